@@ -1,0 +1,315 @@
+#!/usr/bin/env python3
+"""relay's attention + int8 GEMV hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+Prints ONE JSON line. Headline: paged split-context decode
+attention with the fused log-sum-exp merge, 32 sequences x 2048 context, 32 query / 4 KV
+heads, head_dim 64, block size 16, 512-key slices, fp16 Q/K/V ~ N(0, 1), block tables a
+seeded random permutation of the pool. value = algorithmic bytes per launch
+(K + V + Q + O + tables = 67,387,392 B) / average launch time, with inputs resident in
+HBM; the K steps rotate over enough pool copies (> 256 MB) that the 256 MB Infinity
+Cache cannot hold the working set between launches.
+
+Also reported in the same line: flash prefill attention TFLOP/s (config 3's 2048-token
+prompt, 32 / 4 heads, D 64, causal), int8 GEMV GB/s at Llama-3-8B shapes (config 4),
+TinyLlama-1.1B decode tok/s at 32 x 2048 (config 3b, whole forward pass), and the CPU
+oracle's attention on a bounded sample of config 2 (cpu_baseline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+METRIC = "decode-attn HBM GB/s (% peak); prefill-attn TFLOP/s (% MFMA); decode tok/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def run(self, fn, steps, warmup):
+        for i in range(warmup):
+            fn(i)
+        self.torch.cuda.synchronize()
+        a = self.torch.cuda.Event(enable_timing=True)
+        b = self.torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for i in range(steps):
+            fn(warmup + i)
+        b.record(self.stream)
+        self.torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps  # ms per step
+
+
+# ---- config 2: decode attention -------------------------------------------------------
+
+def decode_case(seed, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16):
+    rng = np.random.default_rng(seed)
+    per = ctx // bs
+    nblocks = n_seq * per
+    tables = rng.permutation(nblocks).astype(np.int32)
+    return nblocks, tables
+
+
+def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16, slice_keys=512):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    per = ctx // bs
+    nblocks = n_seq * per
+    pool_bytes = 2 * nblocks * kvh * bs * D * 2
+    copies = max(2, math.ceil(1.5 * MALL_BYTES / pool_bytes) + 1)
+    log(f"decode: {copies} pool copies of {pool_bytes / 1e6:.1f} MB")
+    pools = []
+    for c in range(copies):
+        k = torch.empty(nblocks * kvh * bs * D, dtype=torch.float16, device=dev)
+        v = torch.empty_like(k)
+        _lib.check(L.rh_fill_normal_f16(k.data_ptr(), k.numel(), 1234, 2 * c, 0.0, 1.0, None))
+        _lib.check(L.rh_fill_normal_f16(v.data_ptr(), v.numel(), 1234, 2 * c + 1, 0.0, 1.0, None))
+        tab = torch.from_numpy(np.random.default_rng(c).permutation(nblocks).astype(np.int32)).to(dev)
+        pools.append((k, v, tab))
+    q = torch.empty(n_seq * heads * D, dtype=torch.float16, device=dev)
+    _lib.check(L.rh_fill_normal_f16(q.data_ptr(), q.numel(), 1234, 999, 0.0, 1.0, None))
+    pos = torch.full((n_seq,), ctx - 1, dtype=torch.int32, device=dev)
+    seq = torch.arange(n_seq, dtype=torch.int32, device=dev)
+    toff = torch.arange(n_seq, dtype=torch.int32, device=dev) * per
+    dec = torch.arange(n_seq, dtype=torch.int32, device=dev)
+    parts = math.ceil(ctx / slice_keys)
+    part_o = torch.empty(n_seq * heads * parts * D, dtype=torch.float32, device=dev)
+    part_ml = torch.empty(n_seq * heads * parts * 2, dtype=torch.float32, device=dev)
+    G = heads // kvh
+    counters = torch.zeros(n_seq * kvh * ((G + 15) // 16), dtype=torch.int32, device=dev)
+    out = torch.empty(n_seq * heads * D, dtype=torch.float16, device=dev)
+    torch.cuda.synchronize()
+    sp = stream.cuda_stream
+
+    def step(i):
+        k, v, tab = pools[i % copies]
+        rc = L.rh_paged_decode_attention(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), pos.data_ptr(),
+                                         seq.data_ptr(), toff.data_ptr(), tab.data_ptr(), dec.data_ptr(), n_seq, heads,
+                                         kvh, D, bs, slice_keys, parts, 1.0 / math.sqrt(D), part_o.data_ptr(),
+                                         part_ml.data_ptr(), counters.data_ptr(), out.data_ptr(), heads * D, sp)
+        if rc:
+            raise RuntimeError(_lib.last_error())
+
+    ms = Timer(torch, stream).run(step, steps, warmup)
+    kv_bytes = 2 * n_seq * ctx * kvh * D * 2
+    algo = kv_bytes + 2 * n_seq * heads * D * 2 + n_seq * per * 4
+    return {"ms": ms, "bytes": algo, "gbs": algo / ms / 1e6, "copies": copies}
+
+
+# ---- config 3a: flash prefill attention -----------------------------------------------
+
+def bench_prefill(torch, dev, stream, steps, warmup, S=2048, heads=32, kvh=4, D=64, bs=16):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    nblocks = S // bs
+    k = torch.empty(nblocks * kvh * bs * D, dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    q = torch.empty(S * heads * D, dtype=torch.float16, device=dev)
+    for i, t in enumerate((k, v, q)):
+        _lib.check(L.rh_fill_normal_f16(t.data_ptr(), t.numel(), 77, i, 0.0, 1.0, None))
+    tab = torch.from_numpy(np.random.default_rng(5).permutation(nblocks).astype(np.int32)).to(dev)
+    pos = torch.arange(S, dtype=torch.int32, device=dev)
+    seq = torch.zeros(S, dtype=torch.int32, device=dev)
+    toff = torch.zeros(1, dtype=torch.int32, device=dev)
+    rows = L.rh_prefill_tile_rows()
+    tiles = sorted([(t, min(rows, S - t)) for t in range(0, S, rows)], key=lambda x: -(x[0] + x[1]))
+    tt = torch.tensor([x for t in tiles for x in t], dtype=torch.int32, device=dev)
+    out = torch.empty(S * heads * D, dtype=torch.float16, device=dev)
+    sp = stream.cuda_stream
+
+    def step(i):
+        rc = L.rh_flash_prefill(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), pos.data_ptr(), seq.data_ptr(),
+                                toff.data_ptr(), tab.data_ptr(), tt.data_ptr(), len(tiles), heads, kvh, D, bs,
+                                1.0 / math.sqrt(D), out.data_ptr(), heads * D, sp)
+        if rc:
+            raise RuntimeError(_lib.last_error())
+
+    ms = Timer(torch, stream).run(step, steps, warmup)
+    flops = 4.0 * D * heads * S * (S + 1) / 2
+    return {"ms": ms, "flops": flops, "tflops": flops / ms / 1e9}
+
+
+# ---- config 4: int8 GEMV ---------------------------------------------------------------
+
+GEMV_SHAPES = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]  # (K, N)
+
+
+def bench_gemv(torch, dev, stream, steps, warmup, Ts=(1, 4, 8)):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    res = {}
+    sp = stream.cuda_stream
+    for K, N in GEMV_SHAPES:
+        wbytes = N * K
+        copies = max(2, math.ceil(1.5 * MALL_BYTES / wbytes) + 1)
+        ws = []
+        for c in range(copies):
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            s = (torch.rand(N, device=dev) * 0.019 + 0.001).half()
+            ws.append((w, s))
+        for T in Ts:
+            x = torch.randn(T, K, device=dev).half()
+            y = torch.empty(T, N, device=dev)
+
+            def step(i):
+                w, s = ws[i % copies]
+                rc = L.rh_gemv_int8(w.data_ptr(), s.data_ptr(), 1, x.data_ptr(), y.data_ptr(), T, K, N, 0.0, sp)
+                if rc:
+                    raise RuntimeError(_lib.last_error())
+
+            ms = Timer(torch, stream).run(step, steps, warmup)
+            algo = N * K + 2 * N + 2 * T * K + 4 * T * N
+            res[f"{K}x{N}_T{T}"] = {"us": round(ms * 1e3, 2), "gbs": round(algo / ms / 1e6, 1),
+                                    "frac": round(algo / ms / 1e6 / HBM_PEAK_GBS, 3)}
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
+# ---- config 3b: TinyLlama decode step --------------------------------------------------
+
+def bench_tinyllama_decode(steps, int8=False, n_seq=32, ctx=2048):
+    from relay_amd import HipBackend, HipOptions, tinyllama_1b
+    from relay_amd.backend import ForwardBatch, SeqChunk
+
+    c = tinyllama_1b()
+    bs = 16
+    per = (ctx + 64 + bs - 1) // bs
+    be = HipBackend(None, n_seq * per + 1, bs, max_batch_tokens=512, max_context=per * bs,
+                    options=HipOptions(False, int8), config=c, synthetic_seed=0, synthetic_std=0.02)
+    be.fill_kv_random(seed=3, std=1.0)
+    rng = np.random.default_rng(0)
+    times = []
+    for r in range(steps + 2):
+        batch = ForwardBatch([SeqChunk([int(rng.integers(c.vocab))], ctx + r, list(range(i * per, (i + 1) * per)), True)
+                              for i in range(n_seq)])
+        t0 = time.perf_counter()
+        be.forward(batch)
+        wall = (time.perf_counter() - t0) * 1e3
+        if r >= 2:
+            times.append((wall, be.last_forward_ms()))
+    be.close()
+    wall = float(np.median([t[0] for t in times]))
+    dev_ms = float(np.median([t[1] for t in times]))
+    return {"ms_wall": round(wall, 3), "ms_device": round(dev_ms, 3), "tok_s": round(n_seq / wall * 1e3, 1)}
+
+
+# ---- CPU baseline ----------------------------------------------------------------------
+
+def cpu_baseline(sample_seqs=8, ctx=2048, heads=32, kvh=4, D=64, bs=16):
+    """The CPU oracle's attention (relay's CPU-backend arithmetic) on sample_seqs of
+    config 2's 32 sequences, timed on this host; GB/s of the same fp16 K/V bytes."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    rng = np.random.default_rng(0)
+    per = ctx // bs
+    nb = sample_seqs * per
+    k = rng.standard_normal(nb * kvh * bs * D, dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal(nb * kvh * bs * D, dtype=np.float32).astype(np.float16).astype(np.float32)
+    q = rng.standard_normal((sample_seqs, heads * D), dtype=np.float32).astype(np.float16).astype(np.float32)
+    meta = {"pos": np.full(sample_seqs, ctx - 1, np.int32), "seq": np.arange(sample_seqs, dtype=np.int32),
+            "table_off": (np.arange(sample_seqs) * per).astype(np.int32),
+            "tables": rng.permutation(nb).astype(np.int32)}
+    O.paged_attention(q[:1], heads * D, k, v, {**meta, "pos": meta["pos"][:1]}, None, heads, kvh, D, bs, 0.125)
+    reps, t = 0, 0.0
+    t0 = time.perf_counter()
+    while t < 10.0 and reps < 50:
+        O.paged_attention(q, heads * D, k, v, meta, None, heads, kvh, D, bs, 1.0 / math.sqrt(D))
+        reps += 1
+        t = time.perf_counter() - t0
+    per_call = t / reps
+    byts = 2 * sample_seqs * ctx * kvh * D * 2
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(byts / per_call / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{sample_seqs} of config 2's 32 sequences (ctx {ctx}, 32q/4kv, D64), {reps} calls, "
+                      f"{per_call * 1e3:.1f} ms each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build's hot path (decode/prefill attention, int8 GEMV) runs on one "
+              "MI355X; multi-GPU sharding is described in DESIGN.md and not measured", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from relay_amd import _lib
+
+    _lib.require_device()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+
+    dec = bench_decode(torch, dev, stream, args.steps, args.warmup)
+    log(f"decode attention: {dec['ms'] * 1e3:.2f} us/launch, {dec['gbs']:.0f} GB/s")
+    extra = {}
+    if not args.quick:
+        pre = bench_prefill(torch, dev, stream, max(10, args.steps // 10), 3)
+        log(f"prefill attention: {pre['ms'] * 1e3:.1f} us, {pre['tflops']:.1f} TFLOP/s")
+        extra["prefill_attention"] = {"workload": "2048-token causal prefill, 32q/4kv heads, D64 (config 3)",
+                                      "us": round(pre["ms"] * 1e3, 2), "tflops": round(pre["tflops"], 1),
+                                      "frac_fp16_mfma": round(pre["tflops"] / FP16_PEAK_TFLOPS, 4)}
+        extra["gemv_int8"] = bench_gemv(torch, dev, stream, max(20, args.steps // 4), 5)
+        log(f"gemv: {extra['gemv_int8']}")
+        td = bench_tinyllama_decode(10)
+        log(f"tinyllama decode 32x2048: {td}")
+        extra["tinyllama_decode_32x2048"] = td
+        td8 = bench_tinyllama_decode(10, int8=True)
+        extra["tinyllama_decode_32x2048_int8"] = td8
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(dec["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "paged decode attention, 32 seqs x 2048 ctx, 32q/4kv heads, D64, bs16, "
+                               "512-key slices + fused LSE merge (BASELINE config 2)",
+                   "pool_copies": dec["copies"]},
+        "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

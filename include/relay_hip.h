@@ -1,0 +1,249 @@
+/* relay_hip.h -- the C ABI of relay's MI355X (gfx950) backend.
+ *
+ * Two layers, both plain C: pointers, sizes and a hipStream_t passed as void*.
+ *
+ *  1. Kernel launchers (rh_*). Each takes device pointers that the caller owns and
+ *     enqueues work on `stream` (NULL = the default stream). They return 0, or a
+ *     nonzero code with rh_last_error() describing it (per thread). Shapes are checked
+ *     on the host before anything is launched.
+ *
+ *  2. The backend object (relay_hip_backend_*): the whole forward pass of a Llama/Qwen2
+ *     model over relay's paged KV cache, behind the same contract as relay's C++
+ *     `Backend` interface (engine/include/relay/backend.h:43-81): forward() returns fp32
+ *     logits, KV blocks can be read and written for the transfer engine, weights can be
+ *     updated in place. The C++ class itself (relay::make_hip_backend) is declared in
+ *     relay_amd/csrc/host/relay/backend.h for C++ callers such as relay's Engine.
+ *
+ * Conventions shared with relay (all cited files are in the reference tree):
+ *  - KV cache layout per layer, for K and for V separately (kv_cache.h:20-37):
+ *      [block][kv_head][slot][head_dim], fp16, element offset
+ *      ((block * kv_heads + kv_head) * block_size + slot) * head_dim.
+ *    Token position p of a sequence lives in block table[p / block_size], slot p % block_size.
+ *  - Token metadata (cuda_kernels.cuh:16-21): for each of the T tokens of a step, pos[t]
+ *    and seq[t] (its chunk); table_off[s] is where chunk s's block table starts in the
+ *    concatenated `tables` array.
+ *  - fp16 values are passed as void* holding IEEE binary16.
+ */
+#ifndef RELAY_HIP_H
+#define RELAY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- errors ------------------------------------------------------------------ */
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* rh_last_error(void);
+
+/* 1 if a HIP device is present and usable, else 0 (never fails). */
+int rh_device_available(void);
+
+/* ---- attention over the paged cache ----------------------------------------------- */
+
+/* Split-context decode attention ("flash-decoding") for single-token chunks, with the
+ * log-sum-exp merge of the slices fused in (the last workgroup of a (token, kv head) to
+ * finish merges its slices).
+ * Replaces decode_attention_kernel<D,G> + decode_combine_kernel
+ * (cuda_kernels.cuh:223-339, 341-362) and their launch (cuda_backend.cu:677-686).
+ *
+ *  q           fp16, row t at q + t * q_row_stride (elements), heads * head_dim values
+ *  kpool/vpool fp16 paged cache of ONE layer
+ *  decode_tokens[n_dec]  which tokens of the step are decode tokens
+ *  out         fp16, row t at out + t * out_row_stride, heads * head_dim values
+ *  slice_keys  keys per split (512 in relay); must be a multiple of 128
+ *  max_parts   >= ceil(max context / slice_keys) over the decode tokens
+ *  part_o      fp32 scratch, n_dec * heads * max_parts * head_dim
+ *  part_ml     fp32 scratch, n_dec * heads * max_parts * 2
+ *  counters    int32 scratch, n_dec * kv_heads * ceil((heads / kv_heads) / 16), all ZERO
+ *              before the first call; every call leaves them zero again. Calls that share
+ *              counters must not overlap in time (same stream is fine)
+ *  scale       softmax scale (1/sqrt(head_dim) in relay)
+ * head_dim in {64, 128}; any group size (query heads are processed 16 at a time). */
+int rh_paged_decode_attention(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
+                              const int* pos, const int* seq, const int* table_off, const int* tables,
+                              const int* decode_tokens, int n_dec, int heads, int kv_heads, int head_dim,
+                              int block_size, int slice_keys, int max_parts, float scale, float* part_o,
+                              float* part_ml, int* counters, void* out, int64_t out_row_stride, void* stream);
+
+/* Flash prefill attention for multi-token chunks: causal attention of each tile's query
+ * rows against keys 0..pos of their own sequence, all read from the paged cache (a
+ * chunk at an offset sees the earlier chunks' keys).
+ * Replaces flash_prefill_kernel<D> (cuda_kernels.cuh:37-178) and its launch
+ * (cuda_backend.cu:528-545, 669-676, 689-693).
+ *  tiles       int32 pairs (first token, rows), rows <= rh_prefill_tile_rows(), each
+ *              tile inside one chunk (consecutive positions)
+ * head_dim in {64, 128}. */
+int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool, const int* pos,
+                     const int* seq, const int* table_off, const int* tables, const int* tiles, int n_tiles,
+                     int heads, int kv_heads, int head_dim, int block_size, float scale, void* out,
+                     int64_t out_row_stride, void* stream);
+
+/* Query rows per prefill tile. */
+int rh_prefill_tile_rows(void);
+
+/* Reference attention for any token (decode or prefill), any head_dim <= 256 and any
+ * group size: one workgroup per (token, head), fp32 throughout. The role of relay's M0
+ * kernel (cuda_backend.cu:200-243, RELAY_CUDA_ATTENTION=m0): what the fast kernels are
+ * compared with on the GPU, and the path for head sizes they do not cover.
+ *  q           fp32 (the RoPE'd rows of the qkv buffer), row t at q + t * q_row_stride
+ *  tokens[n]   which tokens to compute (NULL: tokens 0..n-1) */
+int rh_reference_attention(const float* q, int64_t q_row_stride, const void* kpool, const void* vpool,
+                           const int* pos, const int* seq, const int* table_off, const int* tables,
+                           const int* tokens, int n, int heads, int kv_heads, int head_dim, int block_size,
+                           float scale, void* out, int64_t out_row_stride, void* stream);
+
+/* ---- weight-only int8 ----------------------------------------------------------- */
+
+/* y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for
+ * 1 <= T <= 16 tokens. W8 int8 [N, K] row-major; x fp16 [T, K]; y fp32 [T, N].
+ * scale is fp32 [N] (scale_is_f16 = 0, relay's quantizer) or fp16 [N] (scale_is_f16 = 1).
+ * K must be a multiple of 16 and W8 / x 16-byte aligned.
+ * Replaces gemv_int8_kernel<8> (cuda_kernels.cuh:378-430) and its dispatch
+ * (cuda_backend.cu:711-718). */
+int rh_gemv_int8(const int8_t* w8, const void* scale, int scale_is_f16, const void* x, float* y, int T, int K,
+                 int N, float beta, void* stream);
+
+/* Largest T rh_gemv_int8 takes. */
+int rh_gemv_int8_max_tokens(void);
+
+/* Per-row symmetric int8 quantization of an fp32 matrix [N, K] on the device:
+ * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale).
+ * Same values as the reference's host quantizer (cuda_backend.cu:282-304). */
+int rh_quantize_int8(const float* w, int N, int K, int8_t* q, float* scale, void* stream);
+
+/* W16[i] = fp16(W8[i] * scale[i / K]) for a whole [N, K] matrix (the T > 16 path).
+ * Replaces dequant_int8_kernel (cuda_kernels.cuh:432-436). */
+int rh_dequant_int8(const int8_t* w8, const float* scale, int N, int K, void* w16, void* stream);
+
+/* ---- the rest of a transformer layer ------------------------------------------------ */
+
+/* fp32 -> fp16, round to nearest even (bit-identical to relay's f32_to_f16,
+ * safetensors.cpp:65-89). Replaces f32_to_f16_kernel (cuda_backend.cu:112-116). */
+int rh_f32_to_f16(const float* in, void* out, size_t n, void* stream);
+
+/* x[t, :] = fp32(table[tokens[t], :]), table fp16 [vocab, H]. (cuda_backend.cu:150-154) */
+int rh_embed(const int* tokens, int T, const void* table, int H, float* x, void* stream);
+
+/* out[r, :] = fp16(w * (x[rows[r], :] * rsqrt(mean(x^2) + eps))), rows NULL = r itself.
+ * (cuda_backend.cu:157-167) */
+int rh_rmsnorm(const float* x, const int* rows, int R, const float* w, int H, float eps, void* out, void* stream);
+
+/* Per token: qkv row += bias (if not NULL); RoPE on the q and k heads (pairs (i, i + D/2),
+ * angle pos * inv_freq[i]); k and v written as fp16 into the paged cache; q written as
+ * fp16 to q_out (row stride heads * head_dim). (cuda_backend.cu:171-198) */
+int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
+                int kv_heads, int head_dim, int block_size, void* stream);
+
+/* act[t, i] = fp16(g * sigmoid(g) * u), g = gu[t, i], u = gu[t, I + i]. (cuda_backend.cu:245-253) */
+int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream);
+
+/* Pack (gather) or unpack (scatter) one layer's blocks: buf = [K of each listed block]
+ * [V of each listed block], block_bytes a multiple of 16. (cuda_backend.cu:257-270) */
+int rh_kv_gather(const void* kpool, const void* vpool, const int* blocks, int n, size_t block_bytes, void* buf,
+                 void* stream);
+int rh_kv_scatter(void* kpool, void* vpool, const int* blocks, int n, size_t block_bytes, const void* buf,
+                  void* stream);
+
+/* Fills out[i] (i < n) with fp16 / fp32 draws of mean + std * N(0, 1) from the
+ * counter-based generator of rh_synth_normal_f32 (seed, stream, counter i). */
+int rh_fill_normal_f16(void* out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std, void* stream);
+int rh_fill_normal_f32(float* out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std, void* stream);
+
+/* ---- synthetic inputs (host) ------------------------------------------------------ */
+
+/* out[i] = mean + std * z_i, z_i ~ N(0, 1) from splitmix64(seed, stream_id, i) and
+ * Box-Muller in double precision. Deterministic; multithreaded. */
+void rh_synth_normal_f32(float* out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std);
+
+/* ---- the backend object ------------------------------------------------------------ */
+
+/* Model hyperparameters (relay's ModelConfig, config.h). rope_scaling_llama3 = 1 selects
+ * Llama 3 frequency scaling with the four rope_* fields (config.cpp:79-109). */
+typedef struct rh_model_config {
+  int hidden, intermediate, layers, heads, kv_heads, head_dim, vocab, tie_embeddings, qkv_bias;
+  int rope_scaling_llama3;
+  double rms_eps, rope_theta, rope_factor, rope_low_freq_factor, rope_high_freq_factor, rope_original_max_position;
+} rh_model_config;
+
+/* Host fp32 weights in relay's fused layout (weights.h:13-31); pointers per layer.
+ * lm_head NULL when tied to embed; bqkv[l] NULL without q/k/v bias. */
+typedef struct rh_host_weights {
+  const float* embed;      /* [vocab, hidden] */
+  const float* final_norm; /* [hidden] */
+  const float* lm_head;    /* [vocab, hidden] or NULL */
+  const float* const* attn_norm; /* [layers] of [hidden] */
+  const float* const* wqkv;      /* [layers] of [q_dim + 2 kv_dim, hidden] */
+  const float* const* bqkv;      /* [layers] of [q_dim + 2 kv_dim] or NULL */
+  const float* const* wo;        /* [layers] of [hidden, q_dim] */
+  const float* const* mlp_norm;  /* [layers] of [hidden] */
+  const float* const* w_gate_up; /* [layers] of [2 intermediate, hidden] */
+  const float* const* w_down;    /* [layers] of [hidden, intermediate] */
+} rh_host_weights;
+
+/* Options (relay's CudaOptions, backend.h:85-94). reference_attention: the reference
+ * kernel everywhere (RELAY_HIP_ATTENTION=ref). int8_weights: weight-only int8 layers
+ * (RELAY_HIP_INT8=1). */
+typedef struct rh_backend_options {
+  int reference_attention;
+  int int8_weights;
+} rh_backend_options;
+
+/* The options from the environment. */
+rh_backend_options rh_backend_options_from_env(void);
+
+typedef struct relay_hip_backend relay_hip_backend;
+
+/* make_hip_backend (the HIP twin of make_cuda_backend, backend.h:95-97). The weights are
+ * copied to the device; the host arrays may be freed afterwards. NULL on failure. */
+relay_hip_backend* relay_hip_backend_new(const rh_model_config* config, const rh_host_weights* weights,
+                                         int num_blocks, int block_size, int device, int max_batch_tokens,
+                                         int max_context, const rh_backend_options* options);
+
+/* The same model with weights drawn on the device: every matrix and the embedding ~
+ * N(0, std) in fp16 from rh_fill_normal_f16, norms 1, biases 0. For benchmarks of
+ * models too large to build on the host. */
+relay_hip_backend* relay_hip_backend_new_synthetic(const rh_model_config* config, uint64_t seed, float std,
+                                                   int num_blocks, int block_size, int device,
+                                                   int max_batch_tokens, int max_context,
+                                                   const rh_backend_options* options);
+void relay_hip_backend_free(relay_hip_backend* b);
+
+/* Backend::forward (backend.h:50-52) over a batch given as flat arrays: chunk s has
+ * n_tokens[s] tokens (taken in order from `tokens`), starts at start_pos[s], has the block
+ * table of table_len[s] entries (taken in order from `tables`) and want_logits[s].
+ * Logits rows go to `logits` (capacity logits_cap floats); returns the number of rows
+ * (each vocab floats), or -1 on error. */
+int relay_hip_backend_forward(relay_hip_backend* b, int n_seqs, const int* n_tokens, const int* tokens,
+                              const int* start_pos, const int* table_len, const int* tables,
+                              const int* want_logits, int all_logits, float* logits, size_t logits_cap);
+
+/* KV block I/O (backend.h:54-72). Block bytes = kv_heads * block_size * head_dim * 2. */
+size_t relay_hip_backend_kv_block_bytes(const relay_hip_backend* b);
+int relay_hip_backend_read_kv_block(relay_hip_backend* b, int layer, int block, void* k_out, void* v_out);
+int relay_hip_backend_write_kv_block(relay_hip_backend* b, int layer, int block, const void* k_in, const void* v_in);
+int relay_hip_backend_read_kv_layer(relay_hip_backend* b, int layer, const int* blocks, int n, void* out);
+int relay_hip_backend_write_kv_layer(relay_hip_backend* b, int layer, const int* blocks, int n, const void* in);
+int relay_hip_backend_wait_kv_written(relay_hip_backend* b, int layer);
+
+/* Backend::update_weight (backend.h:74-80): `name` as relay names weights, src fp32 in
+ * host memory or device memory of any GPU. */
+int relay_hip_backend_update_weight(relay_hip_backend* b, const char* name, const float* src, size_t n);
+
+/* Fills every layer's K and V cache with N(0, std) fp16 draws (benchmarks that need a
+ * filled cache without running the prompts). */
+int relay_hip_backend_fill_kv_random(relay_hip_backend* b, uint64_t seed, float std);
+
+/* Time in milliseconds of the last forward() measured on the device (HIP events around
+ * the layer loop), for benchmarks. */
+double relay_hip_backend_last_forward_ms(const relay_hip_backend* b);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RELAY_HIP_H */

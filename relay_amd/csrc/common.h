@@ -1,0 +1,108 @@
+// Device-side helpers shared by relay's gfx950 kernels: fp16 vector types, the MFMA
+// instructions the attention and GEMV kernels use, wave-level reductions, and the
+// error plumbing of the C ABI (include/relay_hip.h).
+//
+// MFMA operand layouts on CDNA (wave64), as these kernels rely on them:
+//   v_mfma_f32_16x16x32_f16  D[16x16] += A[16x32] * B[32x16]
+//     A: lane l holds row (l % 16), 8 consecutive k slots of group (l / 16)
+//     B: lane l holds column (l % 16), the same 8 k slots of group (l / 16)
+//     D: lane l holds column (l % 16), rows 4 * (l / 16) + r in register r (r < 4)
+//   v_mfma_f32_32x32x16_f16  D[32x32] += A[32x16] * B[16x32]
+//     A: lane l holds row (l % 32), 8 k slots of group (l / 32)
+//     B: lane l holds column (l % 32), the same 8 k slots of group (l / 32)
+//     D: lane l holds column (l % 32), rows 8 * (r / 4) + 4 * (l / 32) + (r % 4) in
+//        register r (r < 16)
+// Only the row/column placement matters for correctness: the k slot a (group, register)
+// pair stands for is the same for A and B, so the kernels choose which logical k (key or
+// head dimension) each slot carries, as long as both operands agree.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace relay_hip {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef unsigned int uint4v __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float16v mfma32x32x16(half8 a, half8 b, float16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// 16 bytes from global memory as 8 halves (a plain dwordx4 load).
+__device__ __forceinline__ half8 load_half8(const half_t* p) {
+  uint4v v = *reinterpret_cast<const uint4v*>(p);
+  return __builtin_bit_cast(half8, v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Sum over the 4 lanes {l, l^16, l^32, l^48} (the 4 row groups of a 16x16 MFMA tile).
+__device__ __forceinline__ float group4_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// 2^x on the hardware exp unit (v_exp_f32); exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Offset of (position p, kv head) in one layer's paged cache, in elements.
+__device__ __forceinline__ int64_t kv_row_offset(int block, int kv_heads, int kvh, int block_size, int slot, int D) {
+  return ((static_cast<int64_t>(block) * kv_heads + kvh) * block_size + slot) * static_cast<int64_t>(D);
+}
+
+}  // namespace relay_hip
+
+// ---- host-side error plumbing for the C ABI ------------------------------------------
+
+namespace relay_hip {
+void set_error(const std::string& msg);
+}  // namespace relay_hip
+
+#define RH_TRY_LAUNCH(expr)                                                                 \
+  do {                                                                                      \
+    expr;                                                                                   \
+    hipError_t _e = hipGetLastError();                                                      \
+    if (_e != hipSuccess) {                                                                 \
+      relay_hip::set_error(std::string("HIP launch: ") + hipGetErrorString(_e) + " in " + __func__); \
+      return static_cast<int>(_e);                                                          \
+    }                                                                                       \
+  } while (0)
+
+#define RH_REQUIRE(cond, msg)             \
+  do {                                    \
+    if (!(cond)) {                        \
+      relay_hip::set_error(msg);          \
+      return -1;                          \
+    }                                     \
+  } while (0)

@@ -1,0 +1,144 @@
+// Weight-only int8 GEMV for decode batches (T <= 16 tokens) on gfx950.
+//
+//   y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n])
+//
+// relay's gemv_int8_kernel (cuda_kernels.cuh:364-430) does the products on the vector
+// ALU, once per token. Here the products run on the matrix cores instead: a 16-row tile
+// of W is the A operand of v_mfma_f32_16x16x32_f16 and the tokens' activations are the
+// B operand (columns = tokens), so the vector ALU only converts weights, once for all
+// tokens, and the kernel stays bound by the weight stream from HBM at every T.
+//
+// int8 -> fp16 is exact and branch-free: for a byte b, the fp16 with bits
+// 0x6400 | (b ^ 0x80) is 1024 + b + 128, so subtracting 1152 leaves b (all values are
+// integers below 2048, exact in fp16). Products int8 * fp16 are exact in the MFMA's fp32
+// accumulation.
+//
+// Layout of one 64-k chunk of a 16-row tile: lane (c, g) loads the 16 bytes W[n0 + c,
+// k0 + 16g .. +16) -- one 16-byte load per lane, 1 KB per wave -- and splits them into the
+// A operands of two MFMAs (k slots = the two 8-byte halves). Its B operands are the
+// matching 32 bytes of token c's activation row (zero for c >= T). Eight (or sixteen)
+// waves per workgroup split K; their 16x16 accumulators are summed in LDS in a fixed
+// order, so results do not depend on timing.
+#include "../../include/relay_hip.h"
+#include "common.h"
+
+namespace relay_hip {
+namespace {
+
+constexpr int kMaxTokens = 16;
+constexpr int kChunk = 64;   // k per wave step
+constexpr int kUnroll = 4;   // chunks whose loads are issued together
+
+__device__ __forceinline__ half8 int8x8_to_half8(uint32_t lo, uint32_t hi) {
+  // bytes b -> halves with bits 0x6400 | (b ^ 0x80), minus 1152.
+  const uint32_t x0 = lo ^ 0x80808080u, x1 = hi ^ 0x80808080u;
+  uint32_t h[4];
+  h[0] = (x0 & 0xFFu) | ((x0 & 0xFF00u) << 8) | 0x64006400u;
+  h[1] = ((x0 >> 16) & 0xFFu) | ((x0 >> 8) & 0xFF0000u) | 0x64006400u;
+  h[2] = (x1 & 0xFFu) | ((x1 & 0xFF00u) << 8) | 0x64006400u;
+  h[3] = ((x1 >> 16) & 0xFFu) | ((x1 >> 8) & 0xFF0000u) | 0x64006400u;
+  half8 v = __builtin_bit_cast(half8, uint4v{h[0], h[1], h[2], h[3]});
+  const half8 bias = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
+  return v - bias;
+}
+
+template <int WAVES, bool F16_SCALE>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8,
+                                                                  const void* __restrict__ scale,
+                                                                  const half_t* __restrict__ x, float* y, int T,
+                                                                  int K, int N, float beta) {
+  __shared__ float red[WAVES][kWave * 4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int row = min(n0 + c, N - 1);
+  const int nchunks = (K + kChunk - 1) / kChunk;
+  const int per = (nchunks + WAVES - 1) / WAVES;
+  const int cb = w * per, ce = min(nchunks, cb + per);
+  const int8_t* wrow = w8 + static_cast<int64_t>(row) * K;
+  const bool tok = c < T;
+  const half_t* xrow = x + static_cast<int64_t>(tok ? c : 0) * K;
+
+  float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = cb; q0 < ce; q0 += kUnroll) {
+    uint4v wv[kUnroll];
+    half8 xa[kUnroll], xb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int k = (q0 + u) * kChunk + 16 * g;
+      const bool live = q0 + u < ce && k < K;
+      wv[u] = live ? *reinterpret_cast<const uint4v*>(wrow + k) : uint4v{0u, 0u, 0u, 0u};
+      if (live && tok) {
+        xa[u] = load_half8(xrow + k);
+        xb[u] = load_half8(xrow + k + 8);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xa[u][e] = 0;
+          xb[u][e] = 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const half8 a0 = int8x8_to_half8(wv[u][0], wv[u][1]);
+      const half8 a1 = int8x8_to_half8(wv[u][2], wv[u][3]);
+      acc = mfma16x16x32(a0, xa[u], acc);
+      acc = mfma16x16x32(a1, xb[u], acc);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[w][lane * 4 + r] = acc[r];
+  __syncthreads();
+  if (w != 0) return;
+  // Lane (c, g) now sums the waves for token c, rows n0 + 4g + r.
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ww = 0; ww < WAVES; ++ww)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += red[ww][lane * 4 + r];
+  if (!tok) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = n0 + 4 * g + r;
+    if (n >= N) continue;
+    float sc;
+    if (F16_SCALE) sc = static_cast<float>(static_cast<const half_t*>(scale)[n]);
+    else sc = static_cast<const float*>(scale)[n];
+    float* dst = y + static_cast<int64_t>(c) * N + n;
+    *dst = s[r] * sc + (beta != 0.0f ? beta * *dst : 0.0f);
+  }
+}
+
+template <bool F16_SCALE>
+int launch(const int8_t* w8, const void* scale, const half_t* x, float* y, int T, int K, int N, float beta,
+           hipStream_t s) {
+  const int tiles = (N + 15) / 16;
+  if (tiles < 256) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s, w8,
+                                     scale, x, y, T, K, N, beta));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s, w8,
+                                     scale, x, y, T, K, N, beta));
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace relay_hip
+
+using namespace relay_hip;
+
+extern "C" int rh_gemv_int8_max_tokens(void) { return kMaxTokens; }
+
+extern "C" int rh_gemv_int8(const int8_t* w8, const void* scale, int scale_is_f16, const void* x, float* y, int T,
+                            int K, int N, float beta, void* stream) {
+  RH_REQUIRE(T >= 1 && T <= kMaxTokens, "gemv_int8: T must be in 1..16");
+  RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemv_int8: W8 and x must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const half_t* xh = static_cast<const half_t*>(x);
+  return scale_is_f16 ? launch<true>(w8, scale, xh, y, T, K, N, beta, s)
+                      : launch<false>(w8, scale, xh, y, T, K, N, beta, s);
+}

@@ -1,0 +1,643 @@
+// relay's Backend on one MI355X: fp16 (or weight-only int8) weights and KV cache in HBM,
+// fp32 residual stream, the gfx950 kernels of include/relay_hip.h for attention and the
+// int8 GEMV, rocBLAS for the dense fp16 GEMMs.
+//
+// The host orchestration mirrors CudaBackend (engine/src/cuda_backend.cu:311-759) in
+// contract, not in code:
+//  - a forward pass flattens the batch (cuda_backend.cu:508-527), routes single-token
+//    chunks to the split decode kernel and longer chunks to flash prefill tiles
+//    (cuda_backend.cu:528-545), runs the layers, and returns fp32 logits;
+//  - the per-step metadata goes to the device in ONE copy from a pinned buffer (the
+//    reference issues seven), and the prefill tiles are sorted heaviest first so the
+//    causal imbalance does not leave CUs idle at the end of the kernel;
+//  - one event per layer after its KV write backs wait_kv_written, and KV block traffic
+//    runs on a second stream under its own mutex (cuda_backend.cu:611-664).
+// Errors are C++ exceptions as in the reference: std::invalid_argument for bad batches,
+// std::out_of_range for token ids, std::runtime_error("HIP: ...") for runtime failures.
+#include <hip/hip_runtime_api.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+
+#include "relay/backend.h"
+#include "relay_hip.h"
+#include "host_common.h"
+
+namespace relay {
+
+HipOptions HipOptions::from_env() {
+  HipOptions o;
+  if (const char* a = std::getenv("RELAY_HIP_ATTENTION")) o.reference_attention = std::string(a) == "ref";
+  if (const char* q = std::getenv("RELAY_HIP_INT8")) o.int8_weights = std::string(q) == "1";
+  return o;
+}
+
+namespace {
+
+using relay_hip_host::DeviceArray;
+using relay_hip_host::PinnedBuffer;
+
+constexpr int kDecodeSlice = 512;  // keys per decode split (relay's kDecodeSlice)
+
+#define ROCBLAS_CHECK(x)                                                                          \
+  do {                                                                                            \
+    rocblas_status _s = (x);                                                                      \
+    if (_s != rocblas_status_success)                                                             \
+      throw std::runtime_error(std::string("rocBLAS: ") + rocblas_status_to_string(_s) + " at " #x); \
+  } while (0)
+
+// A weight matrix [N, K]: fp16, or int8 with one fp32 scale per row.
+struct DeviceMatrix {
+  int N = 0, K = 0;
+  DeviceArray<std::uint16_t> f16;
+  DeviceArray<std::int8_t> i8;
+  DeviceArray<float> scale;
+};
+
+struct DeviceLayer {
+  DeviceArray<float> attn_norm, mlp_norm, bqkv;
+  DeviceMatrix wqkv, wo, w_gate_up, w_down;
+};
+
+// Where construction takes its weights from: host fp32 arrays (relay's HostWeights
+// layout) or a seeded draw on the device.
+struct WeightSource {
+  const rh_host_weights* host = nullptr;
+  bool synthetic = false;
+  std::uint64_t seed = 0;
+  float std = 0.02f;
+};
+
+class HipBackend final : public Backend {
+ public:
+  HipBackend(const ModelConfig& c, const WeightSource& src, int num_blocks, int block_size, int device,
+             int max_tokens, int max_context, HipOptions options)
+      : c_(c), opt_(options), max_tokens_(max_tokens), max_context_(max_context), device_(device) {
+    if (num_blocks <= 0 || block_size <= 0) throw std::invalid_argument("num_blocks and block_size must be positive");
+    if (max_tokens <= 0) throw std::invalid_argument("max_batch_tokens must be positive");
+    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads) throw std::invalid_argument("bad head counts");
+    HIP_CHECK(hipSetDevice(device));
+    HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    HIP_CHECK(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
+    HIP_CHECK(hipEventCreate(&fwd_begin_));
+    HIP_CHECK(hipEventCreate(&fwd_end_));
+    ROCBLAS_CHECK(rocblas_create_handle(&blas_));
+    ROCBLAS_CHECK(rocblas_set_stream(blas_, stream_));
+    layer_done_.resize(c_.layers);
+    for (auto& e : layer_done_) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    layout_ = {c_.layers, c_.kv_heads, c_.head_dim, block_size, num_blocks};
+    if (kv_block_bytes() % 16 != 0) throw std::invalid_argument("a KV block must be a multiple of 16 bytes");
+    const int D = c_.head_dim;
+    fast_attention_ = !opt_.reference_attention && (D == 64 || D == 128);
+    if (!fast_attention_ && D > 256) throw std::invalid_argument("head_dim above 256 is not supported");
+
+    load_weights(src);
+
+    kc_ = DeviceArray<std::uint16_t>(static_cast<std::size_t>(layout_.layer_elems()) * c_.layers);
+    vc_ = DeviceArray<std::uint16_t>(kc_.n);
+    HIP_CHECK(hipMemset(kc_.p, 0, kc_.n * 2));
+    HIP_CHECK(hipMemset(vc_.p, 0, vc_.n * 2));
+
+    const std::size_t T = max_tokens_;
+    const int H = c_.hidden, QKV = c_.q_dim() + 2 * c_.kv_dim(), I = c_.intermediate;
+    x_ = DeviceArray<float>(T * H);
+    xn_ = DeviceArray<std::uint16_t>(T * std::max(H, I));
+    qkv_ = DeviceArray<float>(T * QKV);
+    qh_ = DeviceArray<std::uint16_t>(T * c_.q_dim());
+    attn_ = DeviceArray<std::uint16_t>(T * c_.q_dim());
+    gu_ = DeviceArray<float>(T * 2 * I);
+    act_ = DeviceArray<std::uint16_t>(T * I);
+    logits_ = DeviceArray<float>(T * c_.vocab);
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
+
+  ~HipBackend() override {
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (copy_stream_) (void)hipStreamSynchronize(copy_stream_);
+    if (blas_) rocblas_destroy_handle(blas_);
+    for (auto e : layer_done_) (void)hipEventDestroy(e);
+    if (fwd_begin_) (void)hipEventDestroy(fwd_begin_);
+    if (fwd_end_) (void)hipEventDestroy(fwd_end_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+    if (copy_stream_) (void)hipStreamDestroy(copy_stream_);
+  }
+
+  const ModelConfig& config() const override { return c_; }
+  const KVLayout& kv_layout() const override { return layout_; }
+  std::string name() const override { return "hip"; }
+  std::size_t kv_block_bytes() const override { return static_cast<std::size_t>(layout_.block_elems()) * 2; }
+
+  double last_forward_ms() const { return last_ms_; }
+
+  void read_kv_block(int layer, int block, void* k_out, void* v_out) override {
+    HIP_CHECK(hipSetDevice(device_));
+    kv_io(layer, {block}, k_out, v_out, nullptr, nullptr);
+  }
+  void write_kv_block(int layer, int block, const void* k_in, const void* v_in) override {
+    HIP_CHECK(hipSetDevice(device_));
+    kv_io(layer, {block}, nullptr, nullptr, k_in, v_in);
+  }
+  void read_kv_layer(int layer, const std::vector<int>& blocks, void* out) override {
+    HIP_CHECK(hipSetDevice(device_));
+    auto* k = static_cast<unsigned char*>(out);
+    kv_io(layer, blocks, k, k + blocks.size() * kv_block_bytes(), nullptr, nullptr);
+  }
+  void write_kv_layer(int layer, const std::vector<int>& blocks, const void* in) override {
+    HIP_CHECK(hipSetDevice(device_));
+    const auto* k = static_cast<const unsigned char*>(in);
+    kv_io(layer, blocks, nullptr, nullptr, k, k + blocks.size() * kv_block_bytes());
+  }
+  void wait_kv_written(int layer) override { HIP_CHECK(hipEventSynchronize(layer_done_.at(layer))); }
+
+  void update_weight(const std::string& name, const float* src, std::size_t n) override;
+
+  void fill_kv_random(std::uint64_t seed, float std) {
+    HIP_CHECK(hipSetDevice(device_));
+    RH_CHECK(rh_fill_normal_f16(kc_.p, kc_.n, seed, 1000001, 0.0f, std, stream_));
+    RH_CHECK(rh_fill_normal_f16(vc_.p, vc_.n, seed, 1000002, 0.0f, std, stream_));
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
+
+  std::vector<float> forward(const ForwardBatch& batch, LayerObserver* observer) override;
+
+ private:
+  void load_weights(const WeightSource& src);
+  DeviceMatrix make_matrix(const float* host, int N, int K, const WeightSource& src, std::uint64_t stream_id);
+  DeviceArray<std::uint16_t> make_f16(const float* host, std::size_t n, const WeightSource& src,
+                                      std::uint64_t stream_id);
+  DeviceArray<float> make_f32(const float* host, std::size_t n, float fill);
+  void upload_f32_rows(const float* host, int N, int K, const std::function<void(const float*, int, int)>& apply);
+  void gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta);
+  void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
+  void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
+
+  ModelConfig c_;
+  HipOptions opt_;
+  bool fast_attention_ = false;
+  KVLayout layout_;
+  int max_tokens_, max_context_, device_;
+  hipStream_t stream_ = nullptr, copy_stream_ = nullptr;
+  rocblas_handle blas_ = nullptr;
+  std::vector<hipEvent_t> layer_done_;
+  hipEvent_t fwd_begin_ = nullptr, fwd_end_ = nullptr;
+  double last_ms_ = 0;
+
+  DeviceArray<std::uint16_t> embed_, lm_head_;
+  DeviceArray<float> final_norm_, inv_freq_;
+  std::vector<DeviceLayer> layers_;
+  DeviceArray<std::uint16_t> kc_, vc_;
+  DeviceArray<float> x_, qkv_, gu_, logits_;
+  DeviceArray<std::uint16_t> xn_, qh_, attn_, act_;
+  DeviceArray<std::uint16_t> dequant_;  // int8 weights widened for a batch above the GEMV's limit
+  std::size_t dequant_elems_ = 0;
+  DeviceArray<float> stage_;            // fp32 staging for uploads and update_weight
+
+  // Per-step metadata: one pinned host buffer, one device buffer, one copy.
+  PinnedBuffer meta_host_;
+  DeviceArray<int> meta_dev_;
+  PinnedBuffer logits_host_;
+  DeviceArray<float> part_o_, part_ml_;
+  DeviceArray<int> counters_;
+
+  std::mutex copy_mu_;
+  DeviceArray<unsigned char> kv_stage_dev_;
+  DeviceArray<int> kv_ids_dev_;
+  PinnedBuffer kv_stage_host_;
+};
+
+void HipBackend::upload_f32_rows(const float* host, int N, int K,
+                                 const std::function<void(const float*, int, int)>& apply) {
+  // Row-aligned chunks of at most 16M floats through the fp32 staging buffer.
+  const std::size_t rows_per = std::max<std::size_t>(1, (std::size_t(16) << 20) / static_cast<std::size_t>(K));
+  const std::size_t need = std::min<std::size_t>(N, rows_per) * K;
+  if (stage_.n < need) stage_ = DeviceArray<float>(need);
+  for (int r0 = 0; r0 < N; r0 += static_cast<int>(rows_per)) {
+    const int rows = std::min<int>(static_cast<int>(rows_per), N - r0);
+    HIP_CHECK(hipMemcpyAsync(stage_.p, host + static_cast<std::size_t>(r0) * K, static_cast<std::size_t>(rows) * K * 4,
+                             hipMemcpyHostToDevice, stream_));
+    apply(stage_.p, r0, rows);
+  }
+}
+
+DeviceArray<std::uint16_t> HipBackend::make_f16(const float* host, std::size_t n, const WeightSource& src,
+                                                std::uint64_t stream_id) {
+  DeviceArray<std::uint16_t> d(n);
+  if (src.synthetic) {
+    RH_CHECK(rh_fill_normal_f16(d.p, n, src.seed, stream_id, 0.0f, src.std, stream_));
+    return d;
+  }
+  // Viewed as rows of 4096 (plus a tail row) for the chunked upload.
+  const int K = 4096;
+  const int full = static_cast<int>(n / K);
+  if (full)
+    upload_f32_rows(host, full, K, [&](const float* chunk, int r0, int rows) {
+      RH_CHECK(rh_f32_to_f16(chunk, d.p + static_cast<std::size_t>(r0) * K, static_cast<std::size_t>(rows) * K, stream_));
+    });
+  const std::size_t tail = n - static_cast<std::size_t>(full) * K;
+  if (tail)
+    upload_f32_rows(host + static_cast<std::size_t>(full) * K, 1, static_cast<int>(tail), [&](const float* chunk, int, int) {
+      RH_CHECK(rh_f32_to_f16(chunk, d.p + static_cast<std::size_t>(full) * K, tail, stream_));
+    });
+  return d;
+}
+
+DeviceArray<float> HipBackend::make_f32(const float* host, std::size_t n, float fill) {
+  DeviceArray<float> d(n);
+  if (!n) return d;
+  if (host) {
+    HIP_CHECK(hipMemcpyAsync(d.p, host, n * 4, hipMemcpyHostToDevice, stream_));
+  } else {
+    std::vector<float> v(n, fill);
+    HIP_CHECK(hipMemcpy(d.p, v.data(), n * 4, hipMemcpyHostToDevice));
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  return d;
+}
+
+DeviceMatrix HipBackend::make_matrix(const float* host, int N, int K, const WeightSource& src,
+                                     std::uint64_t stream_id) {
+  DeviceMatrix m;
+  m.N = N;
+  m.K = K;
+  const std::size_t n = static_cast<std::size_t>(N) * K;
+  if (!opt_.int8_weights) {
+    m.f16 = make_f16(host, n, src, stream_id);
+    return m;
+  }
+  m.i8 = DeviceArray<std::int8_t>(n);
+  m.scale = DeviceArray<float>(N);
+  if (src.synthetic) {
+    // fp32 rows drawn on the device, then the same quantizer as the host-weight path.
+    const std::size_t rows_per = std::max<std::size_t>(1, (std::size_t(16) << 20) / static_cast<std::size_t>(K));
+    if (stage_.n < std::min<std::size_t>(N, rows_per) * K) stage_ = DeviceArray<float>(std::min<std::size_t>(N, rows_per) * K);
+    for (int r0 = 0; r0 < N; r0 += static_cast<int>(rows_per)) {
+      const int rows = std::min<int>(static_cast<int>(rows_per), N - r0);
+      RH_CHECK(rh_fill_normal_f32(stage_.p, static_cast<std::size_t>(rows) * K, src.seed, stream_id * 65536 + r0, 0.0f,
+                                  src.std, stream_));
+      RH_CHECK(rh_quantize_int8(stage_.p, rows, K, m.i8.p + static_cast<std::size_t>(r0) * K, m.scale.p + r0, stream_));
+    }
+  } else {
+    upload_f32_rows(host, N, K, [&](const float* chunk, int r0, int rows) {
+      RH_CHECK(rh_quantize_int8(chunk, rows, K, m.i8.p + static_cast<std::size_t>(r0) * K, m.scale.p + r0, stream_));
+    });
+  }
+  dequant_elems_ = std::max(dequant_elems_, n);
+  return m;
+}
+
+void HipBackend::load_weights(const WeightSource& src) {
+  const int H = c_.hidden, Q = c_.q_dim(), KV = c_.kv_dim(), I = c_.intermediate, V = c_.vocab;
+  const int QKV = Q + 2 * KV;
+  const rh_host_weights* hw = src.host;
+  embed_ = make_f16(hw ? hw->embed : nullptr, static_cast<std::size_t>(V) * H, src, 1);
+  if (!c_.tie_embeddings) {
+    if (hw && !hw->lm_head) throw std::invalid_argument("lm_head is missing and the embeddings are not tied");
+    lm_head_ = make_f16(hw ? hw->lm_head : nullptr, static_cast<std::size_t>(V) * H, src, 2);
+  }
+  final_norm_ = make_f32(hw ? hw->final_norm : nullptr, H, 1.0f);
+  inv_freq_ = make_f32(c_.rope_inv_freq().data(), c_.head_dim / 2, 0.0f);
+  for (int l = 0; l < c_.layers; ++l) {
+    DeviceLayer d;
+    const std::uint64_t sid = 100 + 16 * static_cast<std::uint64_t>(l);
+    d.attn_norm = make_f32(hw ? hw->attn_norm[l] : nullptr, H, 1.0f);
+    d.mlp_norm = make_f32(hw ? hw->mlp_norm[l] : nullptr, H, 1.0f);
+    if (c_.qkv_bias) d.bqkv = make_f32(hw && hw->bqkv ? hw->bqkv[l] : nullptr, QKV, 0.0f);
+    d.wqkv = make_matrix(hw ? hw->wqkv[l] : nullptr, QKV, H, src, sid + 1);
+    d.wo = make_matrix(hw ? hw->wo[l] : nullptr, H, Q, src, sid + 2);
+    d.w_gate_up = make_matrix(hw ? hw->w_gate_up[l] : nullptr, 2 * I, H, src, sid + 3);
+    d.w_down = make_matrix(hw ? hw->w_down[l] : nullptr, H, I, src, sid + 4);
+    layers_.push_back(std::move(d));
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  if (opt_.int8_weights && max_tokens_ > rh_gemv_int8_max_tokens()) dequant_ = DeviceArray<std::uint16_t>(dequant_elems_);
+  stage_ = DeviceArray<float>();  // uploads are done; update_weight reallocates on demand
+}
+
+void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta) {
+  // Row-major y[T, N] = x[T, K] W[N, K]^T is column-major y^T (N x T) = W^T-view (K x N)^T x^T.
+  const float alpha = 1.0f;
+  ROCBLAS_CHECK(rocblas_gemm_ex(blas_, rocblas_operation_transpose, rocblas_operation_none, N, T, K, &alpha, W,
+                                rocblas_datatype_f16_r, K, x, rocblas_datatype_f16_r, K, &beta, y,
+                                rocblas_datatype_f32_r, N, y, rocblas_datatype_f32_r, N, rocblas_datatype_f32_r,
+                                rocblas_gemm_algo_standard, 0, 0));
+}
+
+void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
+  if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
+  if (T <= rh_gemv_int8_max_tokens()) {
+    RH_CHECK(rh_gemv_int8(W.i8.p, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
+    return;
+  }
+  RH_CHECK(rh_dequant_int8(W.i8.p, W.scale.p, W.N, W.K, dequant_.p, stream_));
+  gemm_f16(dequant_.p, x, y, T, W.K, W.N, beta);
+}
+
+std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver* observer) {
+  HIP_CHECK(hipSetDevice(device_));  // the caller's current device may be another GPU
+  const int H = c_.hidden, Q = c_.q_dim(), I = c_.intermediate, D = c_.head_dim, V = c_.vocab;
+  const int QKV = Q + 2 * c_.kv_dim();
+
+  // Flatten (cuda_backend.cu:508-527).
+  std::vector<int> tok, pos, seq, table_off, tables, rows, decode, tiles;
+  std::vector<std::pair<int, int>> tile_work;  // (keys, tile index)
+  const int S = static_cast<int>(batch.seqs.size());
+  int max_ctx = 0;
+  const int tile_rows = rh_prefill_tile_rows();
+  for (int s = 0; s < S; ++s) {
+    const SeqChunk& ch = batch.seqs[s];
+    const int n = static_cast<int>(ch.tokens.size());
+    const int end = ch.start_pos + n;
+    if (static_cast<int>(ch.block_table.size()) < layout_.blocks_for(end))
+      throw std::invalid_argument("block table too short");
+    if (end > max_context_) throw std::invalid_argument("sequence longer than max_context");
+    for (int b : ch.block_table)
+      if (b < 0 || b >= layout_.num_blocks) throw std::invalid_argument("block id outside the cache");
+    table_off.push_back(static_cast<int>(tables.size()));
+    tables.insert(tables.end(), ch.block_table.begin(), ch.block_table.end());
+    const int t0 = static_cast<int>(tok.size());
+    for (int i = 0; i < n; ++i) {
+      if (ch.tokens[i] < 0 || ch.tokens[i] >= V) throw std::out_of_range("token id out of range");
+      if (batch.all_logits) rows.push_back(t0 + i);
+      tok.push_back(ch.tokens[i]);
+      pos.push_back(ch.start_pos + i);
+      seq.push_back(s);
+    }
+    if (!batch.all_logits && ch.want_logits && n > 0) rows.push_back(t0 + n - 1);
+    // Routing: one token -> decode; more -> prefill tiles.
+    if (n == 1) {
+      decode.push_back(t0);
+      max_ctx = std::max(max_ctx, end);
+    } else {
+      for (int r = 0; r < n; r += tile_rows) {
+        const int nr = std::min(tile_rows, n - r);
+        tile_work.push_back({ch.start_pos + r + nr, static_cast<int>(tiles.size() / 2)});
+        tiles.push_back(t0 + r);
+        tiles.push_back(nr);
+      }
+    }
+  }
+  const int T = static_cast<int>(tok.size()), R = static_cast<int>(rows.size());
+  if (T == 0) return {};
+  if (T > max_tokens_) throw std::invalid_argument("batch has more tokens than max_batch_tokens");
+  // Heaviest prefill tile first.
+  std::stable_sort(tile_work.begin(), tile_work.end(), [](auto& a, auto& b) { return a.first > b.first; });
+  std::vector<int> sorted_tiles;
+  sorted_tiles.reserve(tiles.size());
+  for (auto& tw : tile_work) {
+    sorted_tiles.push_back(tiles[2 * tw.second]);
+    sorted_tiles.push_back(tiles[2 * tw.second + 1]);
+  }
+  const int n_dec = static_cast<int>(decode.size()), n_tiles = static_cast<int>(sorted_tiles.size() / 2);
+
+  // One packed metadata copy.
+  const std::size_t o_tok = 0, o_pos = o_tok + T, o_seq = o_pos + T, o_toff = o_seq + T, o_tab = o_toff + S,
+                    o_rows = o_tab + tables.size(), o_dec = o_rows + R, o_tiles = o_dec + n_dec,
+                    total = o_tiles + sorted_tiles.size();
+  meta_host_.reserve(total * sizeof(int));
+  int* mh = static_cast<int*>(meta_host_.p);
+  auto put = [&](std::size_t off, const std::vector<int>& v) { std::copy(v.begin(), v.end(), mh + off); };
+  put(o_tok, tok);
+  put(o_pos, pos);
+  put(o_seq, seq);
+  put(o_toff, table_off);
+  put(o_tab, tables);
+  put(o_rows, rows);
+  put(o_dec, decode);
+  put(o_tiles, sorted_tiles);
+  if (meta_dev_.n < total) meta_dev_ = DeviceArray<int>(total * 2);
+  HIP_CHECK(hipMemcpyAsync(meta_dev_.p, mh, total * sizeof(int), hipMemcpyHostToDevice, stream_));
+  const int* d_tok = meta_dev_.p + o_tok;
+  const int* d_pos = meta_dev_.p + o_pos;
+  const int* d_seq = meta_dev_.p + o_seq;
+  const int* d_toff = meta_dev_.p + o_toff;
+  const int* d_tab = meta_dev_.p + o_tab;
+  const int* d_rows = meta_dev_.p + o_rows;
+  const int* d_dec = meta_dev_.p + o_dec;
+  const int* d_tiles = meta_dev_.p + o_tiles;
+
+  const int parts = n_dec ? (max_ctx + kDecodeSlice - 1) / kDecodeSlice : 0;
+  if (fast_attention_ && n_dec) {
+    const std::size_t need = static_cast<std::size_t>(n_dec) * c_.heads * parts;
+    if (need * D > part_o_.n) part_o_ = DeviceArray<float>(need * D * 2);
+    if (need * 2 > part_ml_.n) part_ml_ = DeviceArray<float>(need * 4);
+    const int G = c_.heads / c_.kv_heads;
+    const std::size_t groups = static_cast<std::size_t>(n_dec) * c_.kv_heads * ((G + 15) / 16);
+    if (groups > counters_.n) {
+      counters_ = DeviceArray<int>(groups * 2);
+      HIP_CHECK(hipMemsetAsync(counters_.p, 0, counters_.n * sizeof(int), stream_));
+    }
+  }
+
+  const float eps = static_cast<float>(c_.rms_eps), scale = 1.0f / std::sqrt(static_cast<float>(D));
+  HIP_CHECK(hipEventRecord(fwd_begin_, stream_));
+  RH_CHECK(rh_embed(d_tok, T, embed_.p, H, x_.p, stream_));
+  for (int l = 0; l < c_.layers; ++l) {
+    DeviceLayer& L = layers_[l];
+    std::uint16_t* kc = kc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
+    std::uint16_t* vc = vc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
+    RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+    gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
+    RH_CHECK(rh_qkv_post(qkv_.p, T, L.bqkv.n ? L.bqkv.p : nullptr, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc,
+                         fast_attention_ ? qh_.p : nullptr, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+    HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
+    if (observer) observer->kv_written(l);
+    if (fast_attention_) {
+      if (n_tiles)
+        RH_CHECK(rh_flash_prefill(qh_.p, Q, kc, vc, d_pos, d_seq, d_toff, d_tab, d_tiles, n_tiles, c_.heads,
+                                  c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
+      if (n_dec)
+        RH_CHECK(rh_paged_decode_attention(qh_.p, Q, kc, vc, d_pos, d_seq, d_toff, d_tab, d_dec, n_dec, c_.heads,
+                                           c_.kv_heads, D, layout_.block_size, kDecodeSlice, parts, scale,
+                                           part_o_.p, part_ml_.p, counters_.p, attn_.p, Q, stream_));
+    } else {
+      RH_CHECK(rh_reference_attention(qkv_.p, QKV, kc, vc, d_pos, d_seq, d_toff, d_tab, nullptr, T, c_.heads,
+                                      c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
+    }
+    gemm(L.wo, attn_.p, x_.p, T, 1.0f);  // x += attn W_o^T
+    RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
+    gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
+    RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
+    gemm(L.w_down, act_.p, x_.p, T, 1.0f);  // x += act W_down^T
+  }
+  std::vector<float> out(static_cast<std::size_t>(R) * V);
+  if (R) {
+    RH_CHECK(rh_rmsnorm(x_.p, d_rows, R, final_norm_.p, H, eps, xn_.p, stream_));
+    gemm_f16(lm_head_.n ? lm_head_.p : embed_.p, xn_.p, logits_.p, R, H, V, 0.0f);
+  }
+  HIP_CHECK(hipEventRecord(fwd_end_, stream_));
+  if (R) {
+    logits_host_.reserve(out.size() * 4);
+    HIP_CHECK(hipMemcpyAsync(logits_host_.p, logits_.p, out.size() * 4, hipMemcpyDeviceToHost, stream_));
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  float ms = 0;
+  HIP_CHECK(hipEventElapsedTime(&ms, fwd_begin_, fwd_end_));
+  last_ms_ = ms;
+  if (R) std::memcpy(out.data(), logits_host_.p, out.size() * 4);
+  return out;
+}
+
+// KV block traffic on the copy stream: gather into a contiguous device buffer, one copy
+// to pinned host memory (and the reverse for writes). Serialised by copy_mu_.
+void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in,
+                       const void* v_in) {
+  if (layer < 0 || layer >= c_.layers) throw std::invalid_argument("layer out of range");
+  for (int b : blocks)
+    if (b < 0 || b >= layout_.num_blocks) throw std::invalid_argument("block id outside the cache");
+  const std::size_t n = blocks.size(), bb = kv_block_bytes();
+  if (!n) return;
+  std::lock_guard<std::mutex> lock(copy_mu_);
+  const std::size_t bytes = 2 * n * bb;
+  if (kv_stage_dev_.n < bytes) kv_stage_dev_ = DeviceArray<unsigned char>(bytes);
+  if (kv_ids_dev_.n < n) kv_ids_dev_ = DeviceArray<int>(n);
+  kv_stage_host_.reserve(bytes + n * sizeof(int));
+  auto* host = static_cast<unsigned char*>(kv_stage_host_.p);
+  auto* ids = reinterpret_cast<int*>(host + bytes);
+  std::memcpy(ids, blocks.data(), n * sizeof(int));
+  HIP_CHECK(hipMemcpyAsync(kv_ids_dev_.p, ids, n * sizeof(int), hipMemcpyHostToDevice, copy_stream_));
+  const std::size_t off = static_cast<std::size_t>(layer) * layout_.layer_elems();
+  if (k_out) {
+    RH_CHECK(rh_kv_gather(kc_.p + off, vc_.p + off, kv_ids_dev_.p, static_cast<int>(n), bb, kv_stage_dev_.p,
+                          copy_stream_));
+    HIP_CHECK(hipMemcpyAsync(host, kv_stage_dev_.p, bytes, hipMemcpyDeviceToHost, copy_stream_));
+    HIP_CHECK(hipStreamSynchronize(copy_stream_));
+    std::memcpy(k_out, host, n * bb);
+    std::memcpy(v_out, host + n * bb, n * bb);
+  } else {
+    std::memcpy(host, k_in, n * bb);
+    std::memcpy(host + n * bb, v_in, n * bb);
+    HIP_CHECK(hipMemcpyAsync(kv_stage_dev_.p, host, bytes, hipMemcpyHostToDevice, copy_stream_));
+    RH_CHECK(rh_kv_scatter(kc_.p + off, vc_.p + off, kv_ids_dev_.p, static_cast<int>(n), bb, kv_stage_dev_.p,
+                           copy_stream_));
+    HIP_CHECK(hipStreamSynchronize(copy_stream_));
+  }
+}
+
+void HipBackend::update_weight(const std::string& name, const float* src, std::size_t n) {
+  HIP_CHECK(hipSetDevice(device_));
+  // src may be host memory, this device's memory, or another GPU's.
+  hipPointerAttribute_t attr{};
+  bool on_device = false;
+  int src_dev = -1;
+  if (hipPointerGetAttributes(&attr, src) == hipSuccess && attr.type == hipMemoryTypeDevice) {
+    on_device = true;
+    src_dev = attr.device;
+  } else {
+    (void)hipGetLastError();
+  }
+  auto chunks = [&](std::size_t total, const std::function<void(const float*, std::size_t, std::size_t)>& apply) {
+    if (n != total) throw std::invalid_argument("update_weight " + name + ": wrong size");
+    if (on_device && src_dev == device_) {
+      apply(src, 0, n);
+      return;
+    }
+    constexpr std::size_t kStage = std::size_t(16) << 20;
+    if (stage_.n < std::min(n, kStage)) stage_ = DeviceArray<float>(std::min(n, kStage));
+    for (std::size_t off = 0; off < n; off += kStage) {
+      const std::size_t len = std::min(kStage, n - off);
+      if (on_device)
+        HIP_CHECK(hipMemcpyPeerAsync(stage_.p, device_, src + off, src_dev, len * 4, stream_));
+      else
+        HIP_CHECK(hipMemcpyAsync(stage_.p, src + off, len * 4, hipMemcpyHostToDevice, stream_));
+      apply(stage_.p, off, len);
+      HIP_CHECK(hipStreamSynchronize(stream_));
+    }
+  };
+  auto to_f16 = [&](DeviceArray<std::uint16_t>& dst) {
+    chunks(dst.n, [&](const float* c, std::size_t off, std::size_t len) { RH_CHECK(rh_f32_to_f16(c, dst.p + off, len, stream_)); });
+  };
+  auto to_f32 = [&](DeviceArray<float>& dst) {
+    chunks(dst.n, [&](const float* c, std::size_t off, std::size_t len) {
+      HIP_CHECK(hipMemcpyAsync(dst.p + off, c, len * 4, hipMemcpyDeviceToDevice, stream_));
+    });
+  };
+  auto matrix = [&](DeviceMatrix& m) {
+    if (m.i8.p) throw std::logic_error("update_weight: int8 weights must be requantized; rebuild the backend");
+    to_f16(m.f16);
+  };
+  if (name == "embed") {
+    to_f16(embed_);
+  } else if (name == "lm_head") {
+    if (!lm_head_.n) throw std::invalid_argument("update_weight: tied embeddings have no lm_head");
+    to_f16(lm_head_);
+  } else if (name == "final_norm") {
+    to_f32(final_norm_);
+  } else if (name.rfind("layers.", 0) == 0) {
+    const std::size_t dot = name.find('.', 7);
+    int i = -1;
+    if (dot != std::string::npos) {
+      try {
+        i = std::stoi(name.substr(7, dot - 7));
+      } catch (const std::exception&) {
+        i = -1;
+      }
+    }
+    if (i < 0 || i >= static_cast<int>(layers_.size())) throw std::invalid_argument("update_weight: no " + name);
+    DeviceLayer& L = layers_[i];
+    const std::string f = name.substr(dot + 1);
+    if (f == "attn_norm") to_f32(L.attn_norm);
+    else if (f == "mlp_norm") to_f32(L.mlp_norm);
+    else if (f == "bqkv" && L.bqkv.n) to_f32(L.bqkv);
+    else if (f == "wqkv") matrix(L.wqkv);
+    else if (f == "wo") matrix(L.wo);
+    else if (f == "w_gate_up") matrix(L.w_gate_up);
+    else if (f == "w_down") matrix(L.w_down);
+    else throw std::invalid_argument("update_weight: no " + name);
+  } else {
+    throw std::invalid_argument("update_weight: no " + name);
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+}  // namespace
+
+// ---- factories ------------------------------------------------------------------------
+
+std::unique_ptr<Backend> make_hip_backend(const HostWeights& w, int num_blocks, int block_size, int device,
+                                          int max_batch_tokens, int max_context, HipOptions options) {
+  const ModelConfig& c = w.config;
+  std::vector<const float*> an, wq, bq, wo, mn, gu, wd;
+  for (const LayerWeights& L : w.layers) {
+    an.push_back(L.attn_norm.data());
+    wq.push_back(L.wqkv.data());
+    bq.push_back(L.bqkv.empty() ? nullptr : L.bqkv.data());
+    wo.push_back(L.wo.data());
+    mn.push_back(L.mlp_norm.data());
+    gu.push_back(L.w_gate_up.data());
+    wd.push_back(L.w_down.data());
+  }
+  rh_host_weights hw{w.embed.data(), w.final_norm.data(), w.lm_head.empty() ? nullptr : w.lm_head.data(),
+                     an.data(), wq.data(), c.qkv_bias ? bq.data() : nullptr, wo.data(), mn.data(), gu.data(), wd.data()};
+  WeightSource src;
+  src.host = &hw;
+  return std::make_unique<HipBackend>(c, src, num_blocks, block_size, device, max_batch_tokens, max_context, options);
+}
+
+namespace hip_detail {
+
+Backend* new_backend(const ModelConfig& c, const rh_host_weights* hw, bool synthetic, std::uint64_t seed, float std,
+                     int num_blocks, int block_size, int device, int max_tokens, int max_context, HipOptions o) {
+  WeightSource src;
+  src.host = hw;
+  src.synthetic = synthetic;
+  src.seed = seed;
+  src.std = std;
+  return new HipBackend(c, src, num_blocks, block_size, device, max_tokens, max_context, o);
+}
+
+double last_forward_ms(const Backend* b) { return static_cast<const HipBackend*>(b)->last_forward_ms(); }
+
+void fill_kv_random(Backend* b, std::uint64_t seed, float std) { static_cast<HipBackend*>(b)->fill_kv_random(seed, std); }
+
+}  // namespace hip_detail
+
+}  // namespace relay

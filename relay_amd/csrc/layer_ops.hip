@@ -1,0 +1,350 @@
+// The small kernels of a transformer layer around the attention and GEMM hot spots:
+// embedding lookup, RMSNorm, bias + RoPE + paged KV write, SiLU-and-multiply, KV block
+// gather/scatter for transfers, fp32 -> fp16 conversion, int8 quantization, and the
+// reference attention kernel. Each cites the reference kernel whose contract it keeps
+// (engine/src/cuda_backend.cu). Also the C ABI's error state and device probe.
+#include <cmath>
+#include <string>
+
+#include "../../include/relay_hip.h"
+#include "common.h"
+
+namespace relay_hip {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const std::string& msg) { g_error = msg; }
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// Sum / max over a workgroup of kThreads; `scratch` holds kThreads / 64 floats.
+template <typename T>
+__device__ T block_sum(T v, T* scratch) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  T r = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) r += scratch[i];
+  __syncthreads();
+  return r;
+}
+
+__device__ float block_max(float v, float* scratch) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float r = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) r = fmaxf(r, scratch[i]);
+  __syncthreads();
+  return r;
+}
+
+__global__ void f32_to_f16_kernel(const float* in, half_t* out, size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[i] = static_cast<half_t>(in[i]);
+}
+
+__global__ void embed_kernel(const int* tokens, const half_t* table, int H, float* x) {
+  const int t = blockIdx.x;
+  const half_t* row = table + static_cast<int64_t>(tokens[t]) * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[static_cast<int64_t>(t) * H + i] = static_cast<float>(row[i]);
+}
+
+// Sum of squares in double, as the fp32 CPU backend does (cpu_backend.cpp:47-52).
+__global__ void rmsnorm_kernel(const float* x, const int* rows, const float* w, int H, float eps, half_t* out) {
+  __shared__ double scratch[kThreads / 64];
+  const int r = blockIdx.x;
+  const float* xr = x + static_cast<int64_t>(rows ? rows[r] : r) * H;
+  double ss = 0;
+  for (int i = threadIdx.x; i < H; i += kThreads) ss += static_cast<double>(xr[i]) * xr[i];
+  ss = block_sum(ss, scratch);
+  const float inv = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
+  for (int i = threadIdx.x; i < H; i += kThreads)
+    out[static_cast<int64_t>(r) * H + i] = static_cast<half_t>(w[i] * (xr[i] * inv));
+}
+
+__global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                                const int* table_off, const int* tables, half_t* kc, half_t* vc, half_t* q_out,
+                                int heads, int kv_heads, int D, int block_size) {
+  const int t = blockIdx.x;
+  const int Q = heads * D, KV = kv_heads * D, QKV = Q + 2 * KV, half = D / 2;
+  float* row = qkv + static_cast<int64_t>(t) * QKV;
+  if (bias)
+    for (int i = threadIdx.x; i < QKV; i += kThreads) row[i] += bias[i];
+  __syncthreads();
+  const int p = pos[t];
+  const int block = tables[table_off[seq[t]] + p / block_size], slot = p % block_size;
+  for (int idx = threadIdx.x; idx < (heads + kv_heads) * half; idx += kThreads) {
+    const int h = idx / half, i = idx % half;
+    float* v = row + h * D;  // q heads, then the k heads that follow them
+    const float angle = static_cast<float>(p) * inv_freq[i];
+    const float cs = cosf(angle), sn = sinf(angle);
+    const float a = v[i], b = v[i + half];
+    v[i] = a * cs - b * sn;
+    v[i + half] = b * cs + a * sn;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < KV; idx += kThreads) {
+    const int h = idx / D, d = idx % D;
+    const int64_t off = kv_row_offset(block, kv_heads, h, block_size, slot, D) + d;
+    kc[off] = static_cast<half_t>(row[Q + idx]);
+    vc[off] = static_cast<half_t>(row[Q + KV + idx]);
+  }
+  if (q_out)
+    for (int idx = threadIdx.x; idx < Q; idx += kThreads) q_out[static_cast<int64_t>(t) * Q + idx] = static_cast<half_t>(row[idx]);
+}
+
+__global__ void silu_mul_kernel(const float* gu, int I, half_t* act) {
+  const int t = blockIdx.x;
+  const float* g = gu + static_cast<int64_t>(t) * 2 * I;
+  const float* u = g + I;
+  for (int i = threadIdx.x; i < I; i += kThreads) {
+    const float v = g[i];
+    act[static_cast<int64_t>(t) * I + i] = static_cast<half_t>(v / (1.0f + expf(-v)) * u[i]);
+  }
+}
+
+__global__ void kv_gather_kernel(const uint4v* k, const uint4v* v, const int* blocks, int n, int64_t vecs, uint4v* out) {
+  const int i = blockIdx.x, which = blockIdx.y;
+  const uint4v* src = (which ? v : k) + static_cast<int64_t>(blocks[i]) * vecs;
+  uint4v* dst = out + (static_cast<int64_t>(which) * n + i) * vecs;
+  for (int64_t e = threadIdx.x; e < vecs; e += kThreads) dst[e] = src[e];
+}
+
+__global__ void kv_scatter_kernel(uint4v* k, uint4v* v, const int* blocks, int n, int64_t vecs, const uint4v* in) {
+  const int i = blockIdx.x, which = blockIdx.y;
+  uint4v* dst = (which ? v : k) + static_cast<int64_t>(blocks[i]) * vecs;
+  const uint4v* src = in + (static_cast<int64_t>(which) * n + i) * vecs;
+  for (int64_t e = threadIdx.x; e < vecs; e += kThreads) dst[e] = src[e];
+}
+
+// One wave per row: scale = max|w| / 127 (1 for a zero row), q = rint(w / scale).
+__global__ void quantize_int8_kernel(const float* w, int N, int K, int8_t* q, float* scale) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const float* row = w + static_cast<int64_t>(n) * K;
+  float mx = 0.0f;
+  for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(row[k]));
+  mx = wave_max(mx);
+  const float s = mx > 0.0f ? mx / 127.0f : 1.0f;
+  if (lane == 0) scale[n] = s;
+  for (int k = lane; k < K; k += 64) q[static_cast<int64_t>(n) * K + k] = static_cast<int8_t>(rintf(row[k] / s));
+}
+
+__global__ void dequant_int8_kernel(const int8_t* w8, const float* scale, int K, int64_t total, half_t* out) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[i] = static_cast<half_t>(static_cast<float>(w8[i]) * scale[i / K]);
+}
+
+// splitmix64 finalizer (Vigna), the mixing function of the synthetic-input generator.
+__device__ __host__ inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ void fill_normal_kernel(T* out, size_t n, uint64_t key, float mean, float std) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const uint64_t a = mix64(key + 0x9E3779B97F4A7C15ull * (2 * i + 1));
+    const uint64_t b = mix64(key + 0x9E3779B97F4A7C15ull * (2 * i + 2));
+    const float u1 = static_cast<float>(((a >> 11) + 1) * (1.0 / 9007199254740992.0));
+    const float u2 = static_cast<float>((b >> 11) * (1.0 / 9007199254740992.0));
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    out[i] = static_cast<T>(mean + std * z);
+  }
+}
+
+// One workgroup per (token, head): keys in chunks of kThreads, each thread scoring one
+// key in fp32, running max and sum across chunks, each thread < D accumulating one output
+// dimension. fp32 q (the RoPE'd qkv rows), fp16 cache; relay's M0 kernel in role
+// (cuda_backend.cu:200-243) without its context limit.
+__global__ void reference_attention_kernel(const float* q, int64_t q_stride, const half_t* kc, const half_t* vc,
+                                           const int* pos, const int* seq, const int* table_off, const int* tables,
+                                           const int* tokens, int heads, int kv_heads, int D, int block_size,
+                                           float scale, half_t* out, int64_t out_stride) {
+  __shared__ float sq[256];
+  __shared__ float sp[kThreads];
+  __shared__ int64_t soff[kThreads];
+  __shared__ float scratch[kThreads / 64];
+  const int t = tokens ? tokens[blockIdx.x] : static_cast<int>(blockIdx.x);
+  const int h = blockIdx.y, kvh = h / (heads / kv_heads);
+  const int ctx = pos[t] + 1;
+  const int* table = tables + table_off[seq[t]];
+  for (int d = threadIdx.x; d < D; d += kThreads) sq[d] = q[static_cast<int64_t>(t) * q_stride + h * D + d];
+  __syncthreads();
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  for (int k0 = 0; k0 < ctx; k0 += kThreads) {
+    const int j = k0 + threadIdx.x;
+    float s = -INFINITY;
+    if (j < ctx) {
+      const int64_t off = kv_row_offset(table[j / block_size], kv_heads, kvh, block_size, j % block_size, D);
+      soff[threadIdx.x] = off;
+      float a = 0.0f;
+      for (int d = 0; d < D; ++d) a += sq[d] * static_cast<float>(kc[off + d]);
+      s = a * scale;
+    }
+    const float cm = block_max(s, scratch);
+    const float m_new = fmaxf(m, cm);
+    const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+    const float p = j < ctx ? expf(s - m_new) : 0.0f;
+    sp[threadIdx.x] = p;
+    const float ps = block_sum(p, scratch);  // also the barrier for sp and soff
+    l = l * alpha + ps;
+    m = m_new;
+    if (threadIdx.x < D) {
+      const int n = min(kThreads, ctx - k0);
+      float a = 0.0f;
+      for (int r = 0; r < n; ++r) a += sp[r] * static_cast<float>(vc[soff[r] + threadIdx.x]);
+      acc = acc * alpha + a;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < D) out[static_cast<int64_t>(t) * out_stride + h * D + threadIdx.x] = static_cast<half_t>(acc / l);
+}
+
+unsigned grid_for(size_t n) { return static_cast<unsigned>(std::min<size_t>((n + kThreads - 1) / kThreads, 8192)); }
+
+}  // namespace
+}  // namespace relay_hip
+
+using namespace relay_hip;
+
+extern "C" {
+
+const char* rh_last_error(void) { return g_error.c_str(); }
+
+int rh_device_available(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n > 0 ? 1 : 0;
+}
+
+int rh_f32_to_f16(const float* in, void* out, size_t n, void* stream) {
+  if (n == 0) return 0;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), in, static_cast<half_t*>(out), n));
+  return 0;
+}
+
+int rh_embed(const int* tokens, int T, const void* table, int H, float* x, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && H > 0, "embed: bad shape");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), tokens,
+                                   static_cast<const half_t*>(table), H, x));
+  return 0;
+}
+
+int rh_rmsnorm(const float* x, const int* rows, int R, const float* w, int H, float eps, void* out, void* stream) {
+  if (R == 0) return 0;
+  RH_REQUIRE(R > 0 && H > 0, "rmsnorm: bad shape");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(kThreads), 0, static_cast<hipStream_t>(stream), x,
+                                   rows, w, H, eps, static_cast<half_t*>(out)));
+  return 0;
+}
+
+int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
+                int kv_heads, int head_dim, int block_size, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
+             "qkv_post: bad shape");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), qkv,
+                                   bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool),
+                                   static_cast<half_t*>(vpool), static_cast<half_t*>(q_out), heads, kv_heads,
+                                   head_dim, block_size));
+  return 0;
+}
+
+int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && I > 0, "silu_mul: bad shape");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(silu_mul_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), gu,
+                                   I, static_cast<half_t*>(act)));
+  return 0;
+}
+
+int rh_kv_gather(const void* kpool, const void* vpool, const int* blocks, int n, size_t block_bytes, void* buf,
+                 void* stream) {
+  if (n == 0) return 0;
+  RH_REQUIRE(n > 0 && block_bytes % 16 == 0, "kv_gather: block bytes must be a multiple of 16");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_gather_kernel, dim3(n, 2), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                                   static_cast<const uint4v*>(kpool), static_cast<const uint4v*>(vpool), blocks, n,
+                                   static_cast<int64_t>(block_bytes / 16), static_cast<uint4v*>(buf)));
+  return 0;
+}
+
+int rh_kv_scatter(void* kpool, void* vpool, const int* blocks, int n, size_t block_bytes, const void* buf,
+                  void* stream) {
+  if (n == 0) return 0;
+  RH_REQUIRE(n > 0 && block_bytes % 16 == 0, "kv_scatter: block bytes must be a multiple of 16");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_scatter_kernel, dim3(n, 2), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                                   static_cast<uint4v*>(kpool), static_cast<uint4v*>(vpool), blocks, n,
+                                   static_cast<int64_t>(block_bytes / 16), static_cast<const uint4v*>(buf)));
+  return 0;
+}
+
+int rh_quantize_int8(const float* w, int N, int K, int8_t* q, float* scale, void* stream) {
+  RH_REQUIRE(N > 0 && K > 0, "quantize_int8: bad shape");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(quantize_int8_kernel, dim3((N + 3) / 4), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), w, N, K, q, scale));
+  return 0;
+}
+
+int rh_dequant_int8(const int8_t* w8, const float* scale, int N, int K, void* w16, void* stream) {
+  RH_REQUIRE(N > 0 && K > 0, "dequant_int8: bad shape");
+  const int64_t total = static_cast<int64_t>(N) * K;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(dequant_int8_kernel, dim3(grid_for(total)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), w8, scale, K, total, static_cast<half_t*>(w16)));
+  return 0;
+}
+
+int rh_fill_normal_f16(void* out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std, void* stream) {
+  if (n == 0) return 0;
+  const uint64_t key = mix64(seed + 0x9E3779B97F4A7C15ull * (stream_id + 1));
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(fill_normal_kernel<half_t>, dim3(grid_for(n)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), static_cast<half_t*>(out), n, key, mean, std));
+  return 0;
+}
+
+int rh_fill_normal_f32(float* out, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std, void* stream) {
+  if (n == 0) return 0;
+  const uint64_t key = mix64(seed + 0x9E3779B97F4A7C15ull * (stream_id + 1));
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(fill_normal_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), out, n, key, mean, std));
+  return 0;
+}
+
+int rh_reference_attention(const float* q, int64_t q_row_stride, const void* kpool, const void* vpool,
+                           const int* pos, const int* seq, const int* table_off, const int* tables,
+                           const int* tokens, int n, int heads, int kv_heads, int head_dim, int block_size,
+                           float scale, void* out, int64_t out_row_stride, void* stream) {
+  if (n == 0) return 0;
+  RH_REQUIRE(n > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "reference attention: bad head counts");
+  RH_REQUIRE(head_dim > 0 && head_dim <= 256, "reference attention: head_dim must be in 1..256");
+  RH_REQUIRE(block_size > 0, "reference attention: bad block size");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(reference_attention_kernel, dim3(n, heads), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), q, q_row_stride,
+                                   static_cast<const half_t*>(kpool), static_cast<const half_t*>(vpool), pos, seq,
+                                   table_off, tables, tokens, heads, kv_heads, head_dim, block_size, scale,
+                                   static_cast<half_t*>(out), out_row_stride));
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+"""Split-context paged decode attention (rh_paged_decode_attention) against the CPU
+oracle, plus the bit-exact properties of block-table gathering.
+
+Oracle: oracle.paged_attention, the fp32 arithmetic of relay's CPU backend
+(cpu_backend.cpp:152-180) on the same fp16 Q/K/V values. Tolerance: the kernel rounds
+the softmax weights and its output to fp16, so |gpu - oracle| <= 2e-3 * max|oracle|
+(fp16's unit roundoff is 4.9e-4).
+Bit-exact: the same logical cache under any block-table permutation, any block size,
+or inside any batch gives identical output bits.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import PagedCase, bits_to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(torch, dev, case, slice_keys=512, tokens=None, counters=None):
+    from relay_amd import _lib
+
+    d = case.to_device(torch, dev)
+    toks = list(range(case.T)) if tokens is None else tokens
+    n = len(toks)
+    H, KVH, D = case.heads, case.kv_heads, case.D
+    G = H // KVH
+    max_parts = max(1, max(math.ceil((case.pos[t] + 1) / slice_keys) for t in toks))
+    dec = torch.tensor(toks, dtype=torch.int32, device=dev)
+    part_o = torch.empty(n * H * max_parts * D, dtype=torch.float32, device=dev)
+    part_ml = torch.empty(n * H * max_parts * 2, dtype=torch.float32, device=dev)
+    if counters is None:
+        counters = torch.zeros(n * KVH * ((G + 15) // 16), dtype=torch.int32, device=dev)
+    out = torch.full((case.T, H * D), float("nan"), dtype=torch.float16, device=dev)
+    print(f"decode case: T={case.T} H={H} KVH={KVH} D={D} bs={case.bs} slice={slice_keys}", flush=True)
+    rc = _lib.lib().rh_paged_decode_attention(
+        d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), d["pos"].data_ptr(), d["seq"].data_ptr(),
+        d["table_off"].data_ptr(), d["tables"].data_ptr(), dec.data_ptr(), n, H, KVH, D, case.bs, slice_keys,
+        max_parts, 1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(), counters.data_ptr(), out.data_ptr(),
+        H * D, None)
+    _lib.check(rc, "rh_paged_decode_attention")
+    torch.cuda.synchronize()
+    res = out.cpu().numpy().astype(np.float32)
+    return res[toks], counters
+
+
+def oracle_out(case, tokens=None):
+    toks = list(range(case.T)) if tokens is None else tokens
+    return O.paged_attention(bits_to_f32(case.q), case.heads * case.D, case.kpool, case.vpool, case.meta, toks,
+                             case.heads, case.kv_heads, case.D, case.bs, 1.0 / math.sqrt(case.D))
+
+
+def check_close(g, o, tol=2e-3):
+    assert np.isfinite(g).all()
+    err = np.abs(g - o).max()
+    assert err <= tol * np.abs(o).max() + 1e-5, f"max abs err {err}, scale {np.abs(o).max()}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 8), (9, 3), (32, 4), (32, 8), (16, 1), (40, 2)])
+def test_matches_oracle_heads(torch_mod, dev, D, heads, kv_heads):
+    case = PagedCase([1, 37, 512, 513, 1500], 1, heads, kv_heads, D, 16, seed=heads + D)
+    g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 31, 32, 33, 127, 128, 129, 511, 512, 513, 1024, 1025, 2048, 3001])
+def test_context_lengths(torch_mod, dev, ctx):
+    case = PagedCase([ctx, max(1, ctx // 3)], 1, 32, 4, 64, 16, seed=ctx)
+    g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
+@pytest.mark.parametrize("slice_keys", [128, 256, 512, 1024])
+def test_slice_sizes(torch_mod, dev, slice_keys):
+    case = PagedCase([100, 700, 2100], 1, 16, 2, 128, 16, seed=slice_keys)
+    g, _ = run_decode(torch_mod, dev, case, slice_keys=slice_keys)
+    check_close(g, oracle_out(case))
+
+
+@pytest.mark.parametrize("bs", [1, 2, 4, 8, 16, 32, 64, 12])
+def test_block_sizes(torch_mod, dev, bs):
+    case = PagedCase([5, 300, 1030], 1, 8, 2, 64, bs, seed=bs)
+    g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
+def _relayout(case, bs, seed):
+    """The same logical K/V rows in a new pool with block size bs and a new permutation."""
+    new = PagedCase([p + 1 for p in case.pos], 1, case.heads, case.kv_heads, case.D, bs, seed=seed)
+    D, KVH = case.D, case.kv_heads
+    for s in range(case.T):
+        ctx = case.pos[s] + 1
+        for p in range(ctx):
+            ob = case.tables[case.table_off[s] + p // case.bs]
+            nb = new.tables[new.table_off[s] + p // bs]
+            for h in range(KVH):
+                o0 = ((ob * KVH + h) * case.bs + p % case.bs) * D
+                n0 = ((nb * KVH + h) * bs + p % bs) * D
+                new.kpool[n0:n0 + D] = case.kpool[o0:o0 + D]
+                new.vpool[n0:n0 + D] = case.vpool[o0:o0 + D]
+    new.q = case.q.copy()
+    return new
+
+
+@pytest.mark.parametrize("bs", [16, 1, 32])
+def test_block_table_gather_is_bit_exact(torch_mod, dev, bs):
+    """Any permutation of the pool's blocks and any block size: identical bits."""
+    case = PagedCase([600, 77, 1200], 1, 32, 4, 64, 16, seed=3)
+    a, _ = run_decode(torch_mod, dev, case)
+    b, _ = run_decode(torch_mod, dev, _relayout(case, bs, seed=99 + bs))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_batch_invariance_is_bit_exact(torch_mod, dev):
+    """A sequence alone or in a batch of others: identical bits."""
+    case = PagedCase([900, 40, 2049, 513], 1, 32, 8, 128, 16, seed=5)
+    together, _ = run_decode(torch_mod, dev, case)
+    for t in range(case.T):
+        alone, _ = run_decode(torch_mod, dev, case, tokens=[t])
+        assert np.array_equal(alone[0].view(np.uint32), together[t].view(np.uint32))
+
+
+def test_repeated_calls_reset_counters(torch_mod, dev):
+    case = PagedCase([1900, 1300], 1, 32, 4, 64, 16, seed=11)
+    a, ctr = run_decode(torch_mod, dev, case)
+    assert int(ctr.abs().sum().item()) == 0
+    b, ctr = run_decode(torch_mod, dev, case, counters=ctr)
+    c, _ = run_decode(torch_mod, dev, case, counters=ctr)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.array_equal(a.view(np.uint32), c.view(np.uint32))
+
+
+def test_config2_full_size(torch_mod, dev):
+    """32 sequences x 2048 context, 32 q / 4 kv heads, D 64, bs 16."""
+    case = PagedCase([2048] * 32, 1, 32, 4, 64, 16, seed=0, extra_blocks=0)
+    g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
+def test_rejects_unsupported_shapes(torch_mod, dev):
+    from relay_amd import _lib
+
+    rc = _lib.lib().rh_paged_decode_attention(None, 64, None, None, None, None, None, None, None, 1, 4, 4, 80, 16,
+                                              512, 1, 0.1, None, None, None, None, 64, None)
+    assert rc != 0 and "head_dim" in _lib.last_error()

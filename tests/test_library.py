@@ -1,0 +1,96 @@
+"""The C-ABI library and the host-side logic, on the CPU (no compute calls on a GPU).
+
+- librelay_hip.so loads and exports every function include/relay_hip.h declares;
+- without a device the package refuses to run (there is no CPU fallback);
+- config parsing matches relay's ModelConfig on the reference fixtures;
+- the synthetic generator is deterministic and has the stated moments;
+- relay's comparison schedule is self-consistent on the CPU oracle (its CPU-vs-CPU
+  run agrees exactly, test_attention.cpp:169-175).
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from relay_amd import _lib
+from relay_amd.model import HostWeights, ModelConfig, llama3_8b, read_safetensors
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "relay_hip.h")
+FIX = os.path.join(REPO, "tests", "golden", "fixtures")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:rh|relay_hip)_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for want in ("rh_paged_decode_attention", "rh_flash_prefill", "rh_gemv_int8", "relay_hip_backend_forward",
+                 "relay_hip_backend_read_kv_layer", "relay_hip_backend_update_weight"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "the ctypes table and the header disagree"
+
+
+def test_no_device_means_an_error_not_a_fallback():
+    if _lib.lib().rh_device_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(_lib.RelayHipError):
+        _lib.require_device()
+    from relay_amd import HipBackend
+
+    w = HostWeights.load(os.path.join(FIX, "llama-mha"))
+    with pytest.raises(_lib.RelayHipError):
+        HipBackend(w, 8, 16)
+
+
+def test_kernel_launchers_validate_shapes_before_launching():
+    lib = _lib.lib()
+    assert lib.rh_gemv_int8(None, None, 0, None, None, 0, 64, 64, 0.0, None) != 0
+    assert "T must be" in _lib.last_error()
+    assert lib.rh_flash_prefill(None, 64, None, None, None, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64,
+                                None) != 0
+    assert lib.rh_prefill_tile_rows() == 128
+    assert lib.rh_gemv_int8_max_tokens() == 16
+
+
+def test_config_parsing_of_the_fixtures():
+    c = ModelConfig.from_json_text(open(os.path.join(FIX, "llama3-rope", "config.json")).read())
+    assert c.rope_llama3 and c.rope_factor > 1
+    q = ModelConfig.from_json_text(open(os.path.join(FIX, "qwen2-bias", "config.json")).read())
+    assert q.qkv_bias
+    g = ModelConfig.from_json_text(open(os.path.join(FIX, "llama-gqa-tied-bf16", "config.json")).read())
+    assert g.tie_embeddings and g.heads > g.kv_heads and g.head_dim == 8
+    t = read_safetensors(os.path.join(FIX, "llama-gqa-tied-bf16", "model.safetensors"))
+    assert all(a.dtype == np.float32 for a in t.values())
+
+
+def test_synthetic_generator_is_deterministic_with_the_stated_moments():
+    n = 1 << 20
+    a, b = np.empty(n, np.float32), np.empty(n, np.float32)
+    _lib.lib().rh_synth_normal_f32(a.ctypes.data, n, 0, 5, 0.0, 0.02)
+    _lib.lib().rh_synth_normal_f32(b.ctypes.data, n, 0, 5, 0.0, 0.02)
+    assert np.array_equal(a, b)
+    c = np.empty(n, np.float32)
+    _lib.lib().rh_synth_normal_f32(c.ctypes.data, n, 0, 6, 0.0, 0.02)
+    assert not np.array_equal(a, c)
+    assert abs(a.mean()) < 5 * 0.02 / np.sqrt(n) and abs(a.std() - 0.02) < 2e-4
+    # the first elements do not depend on n (counter-based, any thread count)
+    s = np.empty(1000, np.float32)
+    _lib.lib().rh_synth_normal_f32(s.ctypes.data, 1000, 0, 5, 0.0, 0.02)
+    assert np.array_equal(s, a[:1000])
+
+
+def test_llama3_config_matches_the_stated_shape():
+    c = llama3_8b()
+    assert (c.hidden, c.layers, c.heads, c.kv_heads, c.head_dim, c.intermediate, c.vocab) == \
+        (4096, 32, 32, 8, 128, 14336, 128256)
