@@ -70,7 +70,8 @@ def decode_case(seed, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16):
     return nblocks, tables
 
 
-def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16, slice_keys=512):
+def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16,
+                 slice_keys=None):
     from relay_amd import _lib
 
     L = _lib.lib()
@@ -89,10 +90,10 @@ def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32
         pools.append((k, v, tab))
     q = torch.empty(n_seq * heads * D, dtype=torch.float16, device=dev)
     _lib.check(L.rh_fill_normal_f16(q.data_ptr(), q.numel(), 1234, 999, 0.0, 1.0, None))
-    pos = torch.full((n_seq,), ctx - 1, dtype=torch.int32, device=dev)
-    seq = torch.arange(n_seq, dtype=torch.int32, device=dev)
-    toff = torch.arange(n_seq, dtype=torch.int32, device=dev) * per
-    dec = torch.arange(n_seq, dtype=torch.int32, device=dev)
+    meta = np.array([[i, ctx, i * per, 0] for i in range(n_seq)], np.int32)
+    dec = torch.from_numpy(meta).to(dev)
+    if slice_keys is None:
+        slice_keys = L.rh_decode_slice_keys(n_seq, kvh, heads // kvh, D, ctx)
     parts = math.ceil(ctx / slice_keys)
     part_o = torch.empty(n_seq * heads * parts * D, dtype=torch.float32, device=dev)
     part_ml = torch.empty(n_seq * heads * parts * 2, dtype=torch.float32, device=dev)
@@ -104,9 +105,9 @@ def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32
 
     def step(i):
         k, v, tab = pools[i % copies]
-        rc = L.rh_paged_decode_attention(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), pos.data_ptr(),
-                                         seq.data_ptr(), toff.data_ptr(), tab.data_ptr(), dec.data_ptr(), n_seq, heads,
-                                         kvh, D, bs, slice_keys, parts, 1.0 / math.sqrt(D), part_o.data_ptr(),
+        rc = L.rh_paged_decode_attention(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), dec.data_ptr(),
+                                         tab.data_ptr(), n_seq, heads, kvh, D, bs, slice_keys, parts,
+                                         1.0 / math.sqrt(D), part_o.data_ptr(),
                                          part_ml.data_ptr(), counters.data_ptr(), out.data_ptr(), heads * D, sp)
         if rc:
             raise RuntimeError(_lib.last_error())
@@ -114,7 +115,7 @@ def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32
     ms = Timer(torch, stream).run(step, steps, warmup)
     kv_bytes = 2 * n_seq * ctx * kvh * D * 2
     algo = kv_bytes + 2 * n_seq * heads * D * 2 + n_seq * per * 4
-    return {"ms": ms, "bytes": algo, "gbs": algo / ms / 1e6, "copies": copies}
+    return {"ms": ms, "bytes": algo, "gbs": algo / ms / 1e6, "copies": copies, "slice_keys": slice_keys}
 
 
 # ---- config 3a: flash prefill attention -----------------------------------------------

@@ -52,9 +52,14 @@ int rh_device_available(void);
  *
  *  q           fp16, row t at q + t * q_row_stride (elements), heads * head_dim values
  *  kpool/vpool fp16 paged cache of ONE layer
- *  decode_tokens[n_dec]  which tokens of the step are decode tokens
+ *  dec_meta    int32 [n_dec][4], 16-byte aligned: per decode token (its row t in q and out,
+ *              its context length = position + 1, the offset of its block table in
+ *              `tables`, unused). The same facts relay's kernel reads through
+ *              pos / seq / table_off (cuda_kernels.cuh:16-26), packed so that a workgroup
+ *              reaches its block table after one load.
  *  out         fp16, row t at out + t * out_row_stride, heads * head_dim values
- *  slice_keys  keys per split (512 in relay); must be a multiple of 128
+ *  slice_keys  keys per split (relay uses 512); a multiple of rh_decode_chunk_keys(head_dim);
+ *              rh_decode_slice_keys() picks one for a step's shape
  *  max_parts   >= ceil(max context / slice_keys) over the decode tokens
  *  part_o      fp32 scratch, n_dec * heads * max_parts * head_dim
  *  part_ml     fp32 scratch, n_dec * heads * max_parts * 2
@@ -64,10 +69,18 @@ int rh_device_available(void);
  *  scale       softmax scale (1/sqrt(head_dim) in relay)
  * head_dim in {64, 128}; any group size (query heads are processed 16 at a time). */
 int rh_paged_decode_attention(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
-                              const int* pos, const int* seq, const int* table_off, const int* tables,
-                              const int* decode_tokens, int n_dec, int heads, int kv_heads, int head_dim,
-                              int block_size, int slice_keys, int max_parts, float scale, float* part_o,
-                              float* part_ml, int* counters, void* out, int64_t out_row_stride, void* stream);
+                              const int* dec_meta, const int* tables, int n_dec, int heads, int kv_heads,
+                              int head_dim, int block_size, int slice_keys, int max_parts, float scale,
+                              float* part_o, float* part_ml, int* counters, void* out, int64_t out_row_stride,
+                              void* stream);
+
+/* Keys per streaming stage of a wave (16 KB of K+V): 64 at head_dim 64, 32 at 128; -1 otherwise. */
+int rh_decode_chunk_keys(int head_dim);
+
+/* The slice_keys rh_paged_decode_attention runs fastest with on MI355X for a step of n_dec
+ * decode tokens whose longest context is max_ctx: whole contexts per workgroup unless
+ * that leaves CUs idle. */
+int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int max_ctx);
 
 /* Flash prefill attention for multi-token chunks: causal attention of each tile's query
  * rows against keys 0..pos of their own sequence, all read from the paged cache (a

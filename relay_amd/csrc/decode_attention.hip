@@ -1,53 +1,57 @@
 // Split-context paged decode attention for gfx950, with the log-sum-exp merge fused in.
 //
 // Work unit: one workgroup per (decode token, kv head, 16-head chunk of its query group,
-// slice of `slice_keys` keys), the split of relay's decode_attention_kernel
-// (cuda_kernels.cuh:180-339). Four waves per workgroup; each wave walks a quarter of the
-// slice in steps of 32 keys:
+// slice of `slice_keys` context keys) -- the split of relay's decode_attention_kernel
+// (cuda_kernels.cuh:180-339). The slice is cut into chunks of 32 KB of K+V (128 keys at
+// head_dim 64, 64 at 128) dealt round-robin to the workgroup's 4 or 8 waves. Per chunk a
+// wave issues every K and V load first (32 KB in flight per wave, ~256 KB per CU), then
+// walks the chunk in steps of 32 keys:
 //
 //   S^T[16 keys x 16 heads] = K[16 keys x D] * Q^T[D x 16 heads]     (MFMA 16x16x32, D/32 per tile)
-//   online softmax per head, in the log2 domain, per lane (lane = head column)
+//   online softmax per head in the log2 domain, per lane (lane = head column)
 //   O^T[D x 16 heads] += V^T[D x 32 keys] * P^T[32 keys x 16 heads]   (MFMA 16x16x32, D/16 tiles)
 //
-// All query heads of the group share one read of each K and V row (the GQA property the
-// reference exploits with its per-thread G-head loop; here the heads are MFMA columns, so
-// the score arithmetic costs no vector-ALU time and the kernel stays bound by HBM).
+// All query heads of the group share one read of each K and V row (relay's kernel does
+// this with a G-head loop per thread; here the heads are MFMA columns, so the score
+// arithmetic costs no vector-ALU time and the kernel stays bound by HBM).
 // K rows go straight from global memory into MFMA A operands: lane (c, g) loads key c of
-// the tile, dims [8g, 8g+8) of each 32-wide group -- a 16-byte load. P^T comes out of the
-// S^T accumulators already in B-operand order (the k slots of the PV product are a
+// the tile, dims [8g, 8g+8) of each 32-wide group -- one 16-byte load. P^T comes out of
+// the S^T accumulators already in B-operand order (the k slots of the PV product are a
 // permutation of the 32 keys, the same for A and B). V needs the transpose V^T, which goes
 // through LDS: each lane writes 16-byte row chunks, then reads single halves in column
 // order; chunks are XOR-swizzled by key so the 4 key groups of a read hit disjoint banks.
 //
-// Loads are issued a round at a time (all of a wave's K and V for ROUND steps, 32 KB per
-// wave), so each CU keeps ~256 KB of HBM reads in flight.
+// Metadata: the host packs, per decode token, (token row, context length, offset of its
+// block table) -- the facts relay's kernel reaches through pos/seq/table_off
+// (cuda_kernels.cuh:16-26, 236-250) -- so a workgroup needs one scalar load before it can
+// read the block table. With a power-of-two block size >= 16 every 16-key tile lies in
+// one block, so its table entry is wave-uniform and read by the scalar unit; other block
+// sizes look entries up per lane. Keys past the context are masked (scores -inf, V rows
+// zeroed).
 //
-// The slices of a (token, kv head) are merged by the last of its workgroups to finish
-// (an atomic counter per group, release/acquire fences at agent scope): no second kernel
-// launch. Slice partials are (M, L) in the log2 domain plus the unnormalized O.
-// Workgroup ids are mapped so the slices of one group land on the same XCD (ids are
-// dealt round-robin over the 8 XCDs), which keeps the merge's reads in one L2.
+// Merging: the waves of a workgroup merge in LDS. When a sequence has several slices, the
+// last of its workgroups to finish merges them (an atomic counter per group; the partials
+// travel through agent-coherent sc1 stores and loads, so no cache-wide fence is needed):
+// no second kernel launch. Slice partials are (M, L) in the log2 domain plus the
+// unnormalized O. Workgroup ids are mapped so the slices of one group land on one XCD
+// (ids are dealt round-robin over the 8 XCDs).
+#include <algorithm>
+
 #include "../../include/relay_hip.h"
 #include "common.h"
 
 namespace relay_hip {
 namespace {
 
-constexpr int kDecWaves = 4;
-constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kStepKeys = 32;
-constexpr int kMaxSliceKeys = 1024;
 
 struct DecodeArgs {
   const half_t* q;
   int64_t q_stride;
   const half_t* kpool;
   const half_t* vpool;
-  const int* pos;
-  const int* seq;
-  const int* table_off;
+  const int4* dec_meta;  // per decode token: (token row, context, table offset, unused)
   const int* tables;
-  const int* decode_tokens;
   int heads, kv_heads, group, hchunks, block_size, bs_shift, slice, max_parts, groups_total;
   float scale_log2;
   float* part_o;
@@ -57,30 +61,56 @@ struct DecodeArgs {
   int64_t out_stride;
 };
 
-__device__ __forceinline__ int block_of(int p, int bs, int shift) { return shift >= 0 ? p >> shift : p / bs; }
-__device__ __forceinline__ int slot_of(int p, int bs, int shift) { return shift >= 0 ? p & (bs - 1) : p % bs; }
+// Stores and loads that are coherent across the device's XCDs for this location (sc1
+// accesses): what the slice merge shares between workgroups.
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Swizzle of a key's 16-byte chunks in the V staging rows.
 __device__ __forceinline__ int vswz(int key) { return ((key >> 2) & 3) << 1; }
 
-template <int D, int ROUND>
-__global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const DecodeArgs a) {
+template <int D>
+constexpr int stage_keys() {
+  return D == 64 ? 128 : 64;
+}
+
+// One chunk of a wave's K and V in registers.
+template <int D>
+struct Stage {
+  static constexpr int STEPS = stage_keys<D>() / kStepKeys;
+  static constexpr int KH = D / 32;
+  static constexpr int VL = kStepKeys * (D / 8) / kWave;
+  half8 k[STEPS][2][KH];
+  half8 v[STEPS][VL];
+};
+
+// SCALAR: block_size is a power of two >= 16 (table entries are wave-uniform per tile).
+template <int D, int WAVES, bool SCALAR>
+__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_decode_kernel(
+    const DecodeArgs a) {
+  constexpr int SK = stage_keys<D>();
+  constexpr int STEPS = SK / kStepKeys;
   constexpr int CH = D / 8;                         // 16-byte chunks per row
   constexpr int KH = D / 32;                        // 32-wide dim groups (QK MFMAs per tile)
   constexpr int DT = D / 16;                        // 16-dim tiles of O^T
   constexpr int VL = kStepKeys * CH / kWave;        // V loads per lane per step
   constexpr int VKEYS = kWave / CH;                 // keys covered by one V load
-  static_assert(kDecWaves * kStepKeys * D * 2 == kDecWaves * 16 * D * 4, "merge area reuses the V staging");
+  constexpr int NT = WAVES * kWave;
+  static_assert(kStepKeys * D * 2 == 16 * D * 4, "the merge area reuses the V staging");
 
-  __shared__ int s_tbl[kMaxSliceKeys + 2];
-  __shared__ __attribute__((aligned(16))) half_t s_v[kDecWaves][kStepKeys * D];
-  __shared__ float s_m[kDecWaves][16], s_l[kDecWaves][16];
+  __shared__ __attribute__((aligned(16))) half_t s_v[WAVES][kStepKeys * D];
+  __shared__ float s_m[WAVES][16], s_l[WAVES][16];
   __shared__ int s_last;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
 
-  // Workgroup -> (group, part), slices of one group on one XCD.
+  // Workgroup -> (group, part), the slices of one group on one XCD.
   const int b = blockIdx.x;
   const int sl = b >> 3;
   const int part = sl % a.max_parts;
@@ -89,87 +119,95 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
   const int per_tok = a.kv_heads * a.hchunks;
   const int di = grp / per_tok;
   const int kvh = (grp % per_tok) / a.hchunks, hc = grp % a.hchunks;
-  const int t = a.decode_tokens[di];
-  const int ctx = a.pos[t] + 1;
+  const int4 meta = a.dec_meta[di];
+  const int t = meta.x, ctx = meta.y;
+  const int* table = a.tables + meta.z;
   const int nparts = (ctx + a.slice - 1) / a.slice;
   if (part >= nparts) return;
   const int begin = part * a.slice, end = min(ctx, begin + a.slice);
   const int h0 = kvh * a.group + hc * 16;
   const int nh = min(16, a.group - hc * 16);
-  const int* table = a.tables + a.table_off[a.seq[t]];
-  const int bs = a.block_size, sh = a.bs_shift;
+  const int bs = a.block_size, sh = a.bs_shift, kvn = a.kv_heads;
 
-  const int fb = block_of(begin, bs, sh), lb = block_of(end - 1, bs, sh);
-  for (int i = threadIdx.x; i <= lb - fb; i += kDecThreads) s_tbl[i] = table[fb + i];
-  __syncthreads();
+  // End of the chunk being computed (keys at or past it are masked).
+  int we_cur = begin;
 
-  // Q^T as B operands: lane (c, g) holds head c, dims [32h + 8g, +8).
-  half8 qb[KH];
+  // Cache row (D elements) of the first slot of a block, for this kv head.
+  auto block_row = [&](int blk) -> unsigned { return static_cast<unsigned>((blk * kvn + kvh) * bs); };
+  // Row of position j (clamped into the context).
+  auto row_any = [&](int j) -> unsigned {
+    j = min(j, end - 1);
+    return block_row(table[j / bs]) + static_cast<unsigned>(j % bs);
+  };
+  // Row of key (tile + off): tile is a 16-aligned wave-uniform position, off < 16 per lane;
+  // the tile's block comes from one scalar table read.
+  auto row_tile = [&](int tile, int off) -> unsigned {
+    const int ts = min(tile, end - 1);
+    const int slot = ts & (bs - 1);
+    return block_row(table[ts >> sh]) + static_cast<unsigned>(min(slot + off, bs - 1));
+  };
+  // Issue every load of the chunk that starts at key k0 (rows first, then the loads).
+  auto issue = [&](Stage<D>& st, int k0) {
+    unsigned krow[STEPS][2], vrow[STEPS][VL];
 #pragma unroll
-  for (int h = 0; h < KH; ++h) {
-    if (c < nh) {
-      qb[h] = load_half8(a.q + static_cast<int64_t>(t) * a.q_stride + static_cast<int64_t>(h0 + c) * D + 32 * h + 8 * g);
-    } else {
+    for (int s = 0; s < STEPS; ++s) {
+      const int ks = k0 + s * kStepKeys;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qb[h][e] = 0;
+      for (int tt = 0; tt < 2; ++tt) krow[s][tt] = SCALAR ? row_tile(ks + 16 * tt, c) : row_any(ks + 16 * tt + c);
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        const int kk = VKEYS * i;  // first key of the load, relative to the step
+        vrow[s][i] = SCALAR ? row_tile(ks + (kk & ~15), (kk & 15) + lane / CH) : row_any(ks + kk + lane / CH);
+      }
     }
-  }
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int h = 0; h < KH; ++h)
+          st.k[s][tt][h] = load_half8(a.kpool + static_cast<int64_t>(krow[s][tt]) * D + 32 * h + 8 * g);
+#pragma unroll
+      for (int i = 0; i < VL; ++i)
+        st.v[s][i] = load_half8(a.vpool + static_cast<int64_t>(vrow[s][i]) * D + 8 * (lane % CH));
+    }
+  };
 
-  const int kpw = a.slice / kDecWaves;
-  const int wb = begin + w * kpw, we = min(end, wb + kpw);
-  const half_t* kbase = a.kpool;
-  const half_t* vbase = a.vpool;
-
+  half_t* sv = s_v[w];
   float m_run = -INFINITY, l_part = 0.0f;
   float4v o[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) o[i] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  half8 qb[KH];
 
-  half_t* sv = s_v[w];
-  for (int r0 = wb; r0 < we; r0 += kStepKeys * ROUND) {
-    half8 kr[ROUND][2][KH];
-    half8 vr[ROUND][VL];
-    // Issue the round's loads, in the order they are consumed.
+  // Online softmax and PV for the chunk at k0 (keys at or past we_cur are masked).
+  auto compute = [&](const Stage<D>& st, int k0) {
 #pragma unroll
-    for (int s = 0; s < ROUND; ++s) {
-      const int k0 = r0 + s * kStepKeys;
-      if (k0 < we) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int j = min(k0 + 16 * tt + c, end - 1);
-          const int64_t off = kv_row_offset(s_tbl[block_of(j, bs, sh) - fb], a.kv_heads, kvh, bs, slot_of(j, bs, sh), D);
-#pragma unroll
-          for (int h = 0; h < KH; ++h) kr[s][tt][h] = load_half8(kbase + off + 32 * h + 8 * g);
-        }
-#pragma unroll
-        for (int i = 0; i < VL; ++i) {
-          const int j = min(k0 + VKEYS * i + lane / CH, end - 1);
-          const int64_t off = kv_row_offset(s_tbl[block_of(j, bs, sh) - fb], a.kv_heads, kvh, bs, slot_of(j, bs, sh), D);
-          vr[s][i] = load_half8(vbase + off + 8 * (lane % CH));
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < ROUND; ++s) {
-      const int k0 = r0 + s * kStepKeys;
-      if (k0 >= we) break;
-      // This step's V rows into the wave's staging area (swizzled 16-byte chunks).
+    for (int s = 0; s < STEPS; ++s) {
+      const int ks = k0 + s * kStepKeys;
+      if (ks >= we_cur) break;
+      // This step's V rows into the wave's staging area (swizzled 16-byte chunks); rows
+      // past the range are zeroed (their weights are 0, their bytes may be anything).
 #pragma unroll
       for (int i = 0; i < VL; ++i) {
         const int kl = VKEYS * i + lane / CH, cc = lane % CH;
-        *reinterpret_cast<half8*>(sv + kl * D + ((cc ^ vswz(kl)) << 3)) = vr[s][i];
+        half8 v = st.v[s][i];
+        if (ks + kl >= we_cur) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0;
+        }
+        *reinterpret_cast<half8*>(sv + kl * D + ((cc ^ vswz(kl)) << 3)) = v;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-      // S^T for the two 16-key tiles.
-      float4v st[2];
+      float4v sc4[2];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        st[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        sc4[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int h = 0; h < KH; ++h) st[tt] = mfma16x16x32(kr[s][tt][h], qb[h], st[tt]);
+        for (int h = 0; h < KH; ++h) sc4[tt] = mfma16x16x32(st.k[s][tt][h], qb[h], sc4[tt]);
       }
       float sc[8];
       float mx = -INFINITY;
@@ -177,8 +215,8 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = k0 + 16 * tt + 4 * g + r;
-          const float v = key < we ? st[tt][r] * a.scale_log2 : -INFINITY;
+          const int key = ks + 16 * tt + 4 * g + r;
+          const float v = key < we_cur ? sc4[tt][r] * a.scale_log2 : -INFINITY;
           sc[tt * 4 + r] = v;
           mx = fmaxf(mx, v);
         }
@@ -216,10 +254,33 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+  };
+
+  // Q once; the first chunk's loads go out before it (Q is needed only at the first MFMA).
+  bool have_q = false;
+  for (int k0 = begin + w * SK; k0 < end; k0 += WAVES * SK) {
+    Stage<D> st;
+    issue(st, k0);
+    if (!have_q) {
+#pragma unroll
+      for (int h = 0; h < KH; ++h) {
+        if (c < nh) {
+          qb[h] = load_half8(a.q + static_cast<int64_t>(t) * a.q_stride + static_cast<int64_t>(h0 + c) * D + 32 * h + 8 * g);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qb[h][e] = 0;
+        }
+      }
+      have_q = true;
+    }
+    // All of the chunk's loads are in flight before any of its arithmetic.
+    __builtin_amdgcn_sched_barrier(0);
+    we_cur = min(end, k0 + SK);
+    compute(st, k0);
   }
   const float l_tot = group4_sum(l_part);
 
-  // Merge the four waves' partials in LDS (the V staging area, now free).
+  // Merge the waves' partials in LDS (the V staging area, now free).
   __syncthreads();
   float* so = reinterpret_cast<float*>(&s_v[0][0]);  // [wave][head][D]
 #pragma unroll
@@ -233,14 +294,14 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
   __syncthreads();
 
   const bool single = nparts == 1;
-  for (int idx = threadIdx.x; idx < nh * D; idx += kDecThreads) {
+  for (int idx = threadIdx.x; idx < nh * D; idx += NT) {
     const int hh = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kDecWaves; ++ww) M = fmaxf(M, s_m[ww][hh]);
+    for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, s_m[ww][hh]);
     float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < kDecWaves; ++ww) {
+    for (int ww = 0; ww < WAVES; ++ww) {
       const float mw = s_m[ww][hh];
       if (mw != -INFINITY) {
         const float f = fast_exp2(mw - M);
@@ -252,40 +313,51 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
       a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * D + d] = static_cast<half_t>(O / L);
     } else {
       const int64_t pb = (static_cast<int64_t>(di) * a.heads + h0 + hh) * a.max_parts + part;
-      a.part_o[pb * D + d] = O;
+      coherent_store(&a.part_o[pb * D + d], O);
       if (d == 0) {
-        a.part_ml[pb * 2] = M;
-        a.part_ml[pb * 2 + 1] = L;
+        coherent_store(&a.part_ml[pb * 2], M);
+        coherent_store(&a.part_ml[pb * 2 + 1], L);
       }
     }
   }
   if (single) return;
 
-  // The last workgroup of this group merges every slice.
-  __threadfence();
+  // The last workgroup of this group merges every slice. Waiting for this workgroup's
+  // coherent stores to complete before the barrier orders them before the counter
+  // increment; the merging workgroup reads the partials with coherent loads.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&a.counters[grp], 1);
+    const int prev = __hip_atomic_fetch_add(&a.counters[grp], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev == nparts - 1;
-    if (last) atomicExch(&a.counters[grp], 0);
+    if (last) __hip_atomic_store(&a.counters[grp], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < nh * D; idx += kDecThreads) {
+  for (int idx = threadIdx.x; idx < nh * D; idx += NT) {
     const int hh = idx / D, d = idx % D;
     const int64_t base = (static_cast<int64_t>(di) * a.heads + h0 + hh) * a.max_parts;
     float M = -INFINITY;
-    for (int p = 0; p < nparts; ++p) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[(base + p) * 2]));
+    for (int p = 0; p < nparts; ++p) M = fmaxf(M, coherent_load(&a.part_ml[(base + p) * 2]));
     float L = 0.0f, O = 0.0f;
     for (int p = 0; p < nparts; ++p) {
-      const float f = fast_exp2(__builtin_nontemporal_load(&a.part_ml[(base + p) * 2]) - M);
-      L += f * __builtin_nontemporal_load(&a.part_ml[(base + p) * 2 + 1]);
-      O += f * __builtin_nontemporal_load(&a.part_o[(base + p) * D + d]);
+      const float f = fast_exp2(coherent_load(&a.part_ml[(base + p) * 2]) - M);
+      L += f * coherent_load(&a.part_ml[(base + p) * 2 + 1]);
+      O += f * coherent_load(&a.part_o[(base + p) * D + d]);
     }
     a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * D + d] = static_cast<half_t>(O / L);
   }
+}
+
+template <int D, int WAVES>
+int launch(const DecodeArgs& a, int grid, hipStream_t s) {
+  if (a.bs_shift >= 4) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<D, WAVES, true>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<D, WAVES, false>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
+  }
+  return 0;
 }
 
 }  // namespace
@@ -293,34 +365,49 @@ __global__ __launch_bounds__(kDecThreads, 2) void paged_decode_kernel(const Deco
 
 using namespace relay_hip;
 
+extern "C" int rh_decode_chunk_keys(int head_dim) {
+  return head_dim == 64 ? stage_keys<64>() : head_dim == 128 ? stage_keys<128>() : -1;
+}
+
+extern "C" int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int max_ctx) {
+  const int chunk = rh_decode_chunk_keys(head_dim);
+  if (chunk <= 0 || n_dec <= 0 || max_ctx <= 0) return chunk;
+  // Measured on MI355X (32 x 2048 / D64 up to 48 x 8192 / D128): at least two slices per
+  // context (enough workgroups to spread over the 256 CUs), more while there are fewer
+  // than 256 (context, kv head) groups, but never below 8 chunks (one per wave of an
+  // 8-wave workgroup).
+  const long groups = static_cast<long>(n_dec) * kv_heads * ((group + 15) / 16);
+  const long parts = std::max(2L, 256 / groups);
+  const long per_part = (max_ctx + parts - 1) / parts;
+  const long keys = std::max(8L * chunk, (per_part + chunk - 1) / chunk * chunk);
+  return static_cast<int>(keys);
+}
+
 extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
-                                         const int* pos, const int* seq, const int* table_off, const int* tables,
-                                         const int* decode_tokens, int n_dec, int heads, int kv_heads, int head_dim,
-                                         int block_size, int slice_keys, int max_parts, float scale, float* part_o,
-                                         float* part_ml, int* counters, void* out, int64_t out_row_stride,
-                                         void* stream) {
+                                         const int* dec_meta, const int* tables, int n_dec, int heads, int kv_heads,
+                                         int head_dim, int block_size, int slice_keys, int max_parts, float scale,
+                                         float* part_o, float* part_ml, int* counters, void* out,
+                                         int64_t out_row_stride, void* stream) {
   if (n_dec == 0) return 0;
   RH_REQUIRE(n_dec > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "decode attention: bad head counts");
   RH_REQUIRE(head_dim == 64 || head_dim == 128, "decode attention: head_dim must be 64 or 128");
   RH_REQUIRE(block_size > 0, "decode attention: bad block size");
-  RH_REQUIRE(slice_keys >= 128 && slice_keys <= kMaxSliceKeys && slice_keys % 128 == 0,
-             "decode attention: slice_keys must be a multiple of 128, at most 1024");
+  const int chunk = rh_decode_chunk_keys(head_dim);
+  RH_REQUIRE(slice_keys >= chunk && slice_keys % chunk == 0,
+             "decode attention: slice_keys must be a positive multiple of rh_decode_chunk_keys(head_dim)");
   RH_REQUIRE(max_parts >= 1, "decode attention: max_parts < 1");
   RH_REQUIRE(q_row_stride % 8 == 0 && out_row_stride >= heads * head_dim,
              "decode attention: q rows must be 16-byte aligned and out rows hold heads * head_dim");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kpool) |
-              reinterpret_cast<uintptr_t>(vpool)) % 16 == 0,
-             "decode attention: q and the pools must be 16-byte aligned");
+              reinterpret_cast<uintptr_t>(vpool) | reinterpret_cast<uintptr_t>(dec_meta)) % 16 == 0,
+             "decode attention: q, the pools and dec_meta must be 16-byte aligned");
   DecodeArgs a;
   a.q = static_cast<const half_t*>(q);
   a.q_stride = q_row_stride;
   a.kpool = static_cast<const half_t*>(kpool);
   a.vpool = static_cast<const half_t*>(vpool);
-  a.pos = pos;
-  a.seq = seq;
-  a.table_off = table_off;
+  a.dec_meta = reinterpret_cast<const int4*>(dec_meta);
   a.tables = tables;
-  a.decode_tokens = decode_tokens;
   a.heads = heads;
   a.kv_heads = kv_heads;
   a.group = heads / kv_heads;
@@ -338,10 +425,8 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
   a.out_stride = out_row_stride;
   const int grid = (a.groups_total + 7) / 8 * 8 * max_parts;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 64) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<64, 4>), dim3(grid), dim3(kDecThreads), 0, s, a));
-  } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<128, 2>), dim3(grid), dim3(kDecThreads), 0, s, a));
-  }
-  return 0;
+  // 8 waves when a slice has at least 8 stages, else 4.
+  const bool eight = slice_keys / chunk >= 8;
+  if (head_dim == 64) return eight ? launch<64, 8>(a, grid, s) : launch<64, 4>(a, grid, s);
+  return eight ? launch<128, 8>(a, grid, s) : launch<128, 4>(a, grid, s);
 }

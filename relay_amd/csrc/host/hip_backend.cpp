@@ -45,7 +45,6 @@ namespace {
 using relay_hip_host::DeviceArray;
 using relay_hip_host::PinnedBuffer;
 
-constexpr int kDecodeSlice = 512;  // keys per decode split (relay's kDecodeSlice)
 
 #define ROCBLAS_CHECK(x)                                                                          \
   do {                                                                                            \
@@ -374,7 +373,8 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     if (!batch.all_logits && ch.want_logits && n > 0) rows.push_back(t0 + n - 1);
     // Routing: one token -> decode; more -> prefill tiles.
     if (n == 1) {
-      decode.push_back(t0);
+      // (token row, context length, block-table offset): the decode kernel's descriptor
+      decode.insert(decode.end(), {t0, end, table_off.back(), 0});
       max_ctx = std::max(max_ctx, end);
     } else {
       for (int r = 0; r < n; r += tile_rows) {
@@ -396,11 +396,12 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     sorted_tiles.push_back(tiles[2 * tw.second]);
     sorted_tiles.push_back(tiles[2 * tw.second + 1]);
   }
-  const int n_dec = static_cast<int>(decode.size()), n_tiles = static_cast<int>(sorted_tiles.size() / 2);
+  const int n_dec = static_cast<int>(decode.size() / 4), n_tiles = static_cast<int>(sorted_tiles.size() / 2);
 
   // One packed metadata copy.
-  const std::size_t o_tok = 0, o_pos = o_tok + T, o_seq = o_pos + T, o_toff = o_seq + T, o_tab = o_toff + S,
-                    o_rows = o_tab + tables.size(), o_dec = o_rows + R, o_tiles = o_dec + n_dec,
+  // The decode descriptors come first: 16-byte aligned.
+  const std::size_t o_dec = 0, o_tok = o_dec + decode.size(), o_pos = o_tok + T, o_seq = o_pos + T,
+                    o_toff = o_seq + T, o_tab = o_toff + S, o_rows = o_tab + tables.size(), o_tiles = o_rows + R,
                     total = o_tiles + sorted_tiles.size();
   meta_host_.reserve(total * sizeof(int));
   int* mh = static_cast<int*>(meta_host_.p);
@@ -424,7 +425,12 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   const int* d_dec = meta_dev_.p + o_dec;
   const int* d_tiles = meta_dev_.p + o_tiles;
 
-  const int parts = n_dec ? (max_ctx + kDecodeSlice - 1) / kDecodeSlice : 0;
+  // Keys per decode split: relay fixes 512 (cuda_kernels.cuh:190); here the planner picks
+  // the split for this step's shape (results differ only by rounding).
+  const int slice = fast_attention_ && n_dec
+                        ? rh_decode_slice_keys(n_dec, c_.kv_heads, c_.heads / c_.kv_heads, D, max_ctx)
+                        : 0;
+  const int parts = n_dec && slice > 0 ? (max_ctx + slice - 1) / slice : 0;
   if (fast_attention_ && n_dec) {
     const std::size_t need = static_cast<std::size_t>(n_dec) * c_.heads * parts;
     if (need * D > part_o_.n) part_o_ = DeviceArray<float>(need * D * 2);
@@ -455,8 +461,8 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
         RH_CHECK(rh_flash_prefill(qh_.p, Q, kc, vc, d_pos, d_seq, d_toff, d_tab, d_tiles, n_tiles, c_.heads,
                                   c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
       if (n_dec)
-        RH_CHECK(rh_paged_decode_attention(qh_.p, Q, kc, vc, d_pos, d_seq, d_toff, d_tab, d_dec, n_dec, c_.heads,
-                                           c_.kv_heads, D, layout_.block_size, kDecodeSlice, parts, scale,
+        RH_CHECK(rh_paged_decode_attention(qh_.p, Q, kc, vc, d_dec, d_tab, n_dec, c_.heads,
+                                           c_.kv_heads, D, layout_.block_size, slice, parts, scale,
                                            part_o_.p, part_ml_.p, counters_.p, attn_.p, Q, stream_));
     } else {
       RH_CHECK(rh_reference_attention(qkv_.p, QKV, kc, vc, d_pos, d_seq, d_toff, d_tab, nullptr, T, c_.heads,

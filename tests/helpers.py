@@ -41,6 +41,11 @@ class PagedCase:
         self.meta = {"pos": np.array(self.pos, np.int32), "seq": np.array(self.seq, np.int32),
                      "table_off": np.array(self.table_off, np.int32), "tables": np.array(self.tables, np.int32)}
 
+    def dec_meta(self, tokens=None) -> np.ndarray:
+        """rh_paged_decode_attention's descriptors: (row, context, table offset, 0) per token."""
+        toks = range(self.T) if tokens is None else tokens
+        return np.array([[t, self.pos[t] + 1, self.table_off[self.seq[t]], 0] for t in toks], np.int32)
+
     def to_device(self, torch, dev):
         t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(dev) if dt is None else \
             torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)

@@ -19,7 +19,8 @@ from helpers import PagedCase, bits_to_f32
 pytestmark = pytest.mark.gpu
 
 
-def run_decode(torch, dev, case, slice_keys=512, tokens=None, counters=None):
+def run_decode(torch, dev, case, slice_keys=None, tokens=None, counters=None):
+    """slice_keys None: the planner's choice (rh_decode_slice_keys)."""
     from relay_amd import _lib
 
     d = case.to_device(torch, dev)
@@ -27,8 +28,10 @@ def run_decode(torch, dev, case, slice_keys=512, tokens=None, counters=None):
     n = len(toks)
     H, KVH, D = case.heads, case.kv_heads, case.D
     G = H // KVH
+    if slice_keys is None:
+        slice_keys = _lib.lib().rh_decode_slice_keys(n, KVH, G, D, max(case.pos[t] + 1 for t in toks))
     max_parts = max(1, max(math.ceil((case.pos[t] + 1) / slice_keys) for t in toks))
-    dec = torch.tensor(toks, dtype=torch.int32, device=dev)
+    dec = torch.from_numpy(case.dec_meta(toks)).to(dev)
     part_o = torch.empty(n * H * max_parts * D, dtype=torch.float32, device=dev)
     part_ml = torch.empty(n * H * max_parts * 2, dtype=torch.float32, device=dev)
     if counters is None:
@@ -36,10 +39,9 @@ def run_decode(torch, dev, case, slice_keys=512, tokens=None, counters=None):
     out = torch.full((case.T, H * D), float("nan"), dtype=torch.float16, device=dev)
     print(f"decode case: T={case.T} H={H} KVH={KVH} D={D} bs={case.bs} slice={slice_keys}", flush=True)
     rc = _lib.lib().rh_paged_decode_attention(
-        d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), d["pos"].data_ptr(), d["seq"].data_ptr(),
-        d["table_off"].data_ptr(), d["tables"].data_ptr(), dec.data_ptr(), n, H, KVH, D, case.bs, slice_keys,
-        max_parts, 1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(), counters.data_ptr(), out.data_ptr(),
-        H * D, None)
+        d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), dec.data_ptr(), d["tables"].data_ptr(), n,
+        H, KVH, D, case.bs, slice_keys, max_parts, 1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(),
+        counters.data_ptr(), out.data_ptr(), H * D, None)
     _lib.check(rc, "rh_paged_decode_attention")
     torch.cuda.synchronize()
     res = out.cpu().numpy().astype(np.float32)
@@ -73,9 +75,11 @@ def test_context_lengths(torch_mod, dev, ctx):
     check_close(g, oracle_out(case))
 
 
-@pytest.mark.parametrize("slice_keys", [128, 256, 512, 1024])
-def test_slice_sizes(torch_mod, dev, slice_keys):
-    case = PagedCase([100, 700, 2100], 1, 16, 2, 128, 16, seed=slice_keys)
+@pytest.mark.parametrize("D,slice_keys", [(64, 128), (64, 384), (64, 512), (64, 1024), (64, 2048), (64, 4096),
+                                          (128, 64), (128, 192), (128, 512), (128, 1024), (128, 4096)])
+def test_slice_sizes(torch_mod, dev, D, slice_keys):
+    """Every split of the context (1 to 66 slices; 4 or 8 waves) gives the same attention."""
+    case = PagedCase([100, 700, 2100], 1, 16, 2, D, 16, seed=slice_keys)
     g, _ = run_decode(torch_mod, dev, case, slice_keys=slice_keys)
     check_close(g, oracle_out(case))
 
@@ -109,39 +113,45 @@ def _relayout(case, bs, seed):
 def test_block_table_gather_is_bit_exact(torch_mod, dev, bs):
     """Any permutation of the pool's blocks and any block size: identical bits."""
     case = PagedCase([600, 77, 1200], 1, 32, 4, 64, 16, seed=3)
-    a, _ = run_decode(torch_mod, dev, case)
-    b, _ = run_decode(torch_mod, dev, _relayout(case, bs, seed=99 + bs))
+    a, _ = run_decode(torch_mod, dev, case, slice_keys=512)
+    b, _ = run_decode(torch_mod, dev, _relayout(case, bs, seed=99 + bs), slice_keys=512)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_batch_invariance_is_bit_exact(torch_mod, dev):
     """A sequence alone or in a batch of others: identical bits."""
     case = PagedCase([900, 40, 2049, 513], 1, 32, 8, 128, 16, seed=5)
-    together, _ = run_decode(torch_mod, dev, case)
+    together, _ = run_decode(torch_mod, dev, case, slice_keys=512)
     for t in range(case.T):
-        alone, _ = run_decode(torch_mod, dev, case, tokens=[t])
+        alone, _ = run_decode(torch_mod, dev, case, tokens=[t], slice_keys=512)
         assert np.array_equal(alone[0].view(np.uint32), together[t].view(np.uint32))
 
 
 def test_repeated_calls_reset_counters(torch_mod, dev):
     case = PagedCase([1900, 1300], 1, 32, 4, 64, 16, seed=11)
-    a, ctr = run_decode(torch_mod, dev, case)
+    a, ctr = run_decode(torch_mod, dev, case, slice_keys=256)
     assert int(ctr.abs().sum().item()) == 0
-    b, ctr = run_decode(torch_mod, dev, case, counters=ctr)
-    c, _ = run_decode(torch_mod, dev, case, counters=ctr)
+    b, ctr = run_decode(torch_mod, dev, case, counters=ctr, slice_keys=256)
+    c, _ = run_decode(torch_mod, dev, case, counters=ctr, slice_keys=256)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.array_equal(a.view(np.uint32), c.view(np.uint32))
 
 
 def test_config2_full_size(torch_mod, dev):
     """32 sequences x 2048 context, 32 q / 4 kv heads, D 64, bs 16."""
     case = PagedCase([2048] * 32, 1, 32, 4, 64, 16, seed=0, extra_blocks=0)
-    g, _ = run_decode(torch_mod, dev, case)
-    check_close(g, oracle_out(case))
+    want = oracle_out(case)
+    for sk in (None, 512):
+        g, _ = run_decode(torch_mod, dev, case, slice_keys=sk)
+        check_close(g, want)
 
 
 def test_rejects_unsupported_shapes(torch_mod, dev):
     from relay_amd import _lib
 
-    rc = _lib.lib().rh_paged_decode_attention(None, 64, None, None, None, None, None, None, None, 1, 4, 4, 80, 16,
-                                              512, 1, 0.1, None, None, None, None, 64, None)
+    L = _lib.lib()
+    rc = L.rh_paged_decode_attention(None, 64, None, None, None, None, 1, 4, 4, 80, 16, 512, 1, 0.1, None, None, None,
+                                     None, 64, None)
     assert rc != 0 and "head_dim" in _lib.last_error()
+    rc = L.rh_paged_decode_attention(None, 256, None, None, None, None, 1, 4, 4, 64, 16, 100, 1, 0.1, None, None, None,
+                                     None, 256, None)
+    assert rc != 0 and "slice_keys" in _lib.last_error()

@@ -157,10 +157,12 @@ def test_qkv_post_rope_matches_oracle(torch_mod, dev):
         tables.extend([0] * (p // bs + 1))
     kc = torch_mod.zeros(kvh * bs * D, dtype=torch_mod.int16, device=dev)
     vc = torch_mod.zeros_like(kc)
-    _lib.check(_lib.lib().rh_qkv_post(X.data_ptr(), T, None, dt(inv).data_ptr(), dt(np.array(pos, np.int32)).data_ptr(),
-                                      dt(np.arange(T, dtype=np.int32)).data_ptr(),
-                                      dt(np.array(toff, np.int32)).data_ptr(),
-                                      dt(np.array(tables, np.int32)).data_ptr(), kc.data_ptr(), vc.data_ptr(), None,
+    # keep every device buffer referenced until the kernel has run (a temporary's memory
+    # goes back to torch's caching allocator as soon as its data_ptr() is taken)
+    INV, POS, SEQ = dt(inv), dt(np.array(pos, np.int32)), dt(np.arange(T, dtype=np.int32))
+    TOFF, TABS = dt(np.array(toff, np.int32)), dt(np.array(tables, np.int32))
+    _lib.check(_lib.lib().rh_qkv_post(X.data_ptr(), T, None, INV.data_ptr(), POS.data_ptr(), SEQ.data_ptr(),
+                                      TOFF.data_ptr(), TABS.data_ptr(), kc.data_ptr(), vc.data_ptr(), None,
                                       heads, kvh, D, bs, None))
     torch_mod.cuda.synchronize()
     got = X.cpu().numpy()
