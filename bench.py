@@ -250,6 +250,21 @@ def cpu_baseline(sample_seqs=8, ctx=2048, heads=32, kvh=4, D=64, bs=16):
                       f"{per_call * 1e3:.1f} ms each"}
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_attention_config2_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode kernel, from the rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE runs summarised in profiles/ (scaled by the copy-kernel calibration there);
+    None until that summary exists."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(float(line.split("=")[1]))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,6 +272,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's hot path (decode/prefill attention, int8 GEMV) runs on one "
@@ -270,6 +288,14 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
+    if args.calibrate_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": 256 << 20, "launches": 20}))
+        return
 
     dec = bench_decode(torch, dev, stream, args.steps, args.warmup)
     log(f"decode attention: {dec['ms'] * 1e3:.2f} us/launch, {dec['gbs']:.0f} GB/s")
@@ -301,11 +327,11 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "paged decode attention, 32 seqs x 2048 ctx, 32q/4kv heads, D64, bs16, "
-                               "512-key slices + fused LSE merge (BASELINE config 2)",
-                   "pool_copies": dec["copies"]},
+        "config": {"workload": "paged decode attention, 32 seqs x 2048 ctx, 32q/4kv heads, D64, bs16, split "
+                               "context + fused LSE merge (BASELINE config 2)",
+                   "slice_keys": dec["slice_keys"], "pool_copies": dec["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         **extra,
     }
