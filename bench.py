@@ -131,19 +131,13 @@ def bench_prefill(torch, dev, stream, steps, warmup, S=2048, heads=32, kvh=4, D=
     for i, t in enumerate((k, v, q)):
         _lib.check(L.rh_fill_normal_f16(t.data_ptr(), t.numel(), 77, i, 0.0, 1.0, None))
     tab = torch.from_numpy(np.random.default_rng(5).permutation(nblocks).astype(np.int32)).to(dev)
-    pos = torch.arange(S, dtype=torch.int32, device=dev)
-    seq = torch.zeros(S, dtype=torch.int32, device=dev)
-    toff = torch.zeros(1, dtype=torch.int32, device=dev)
-    rows = L.rh_prefill_tile_rows()
-    tiles = sorted([(t, min(rows, S - t)) for t in range(0, S, rows)], key=lambda x: -(x[0] + x[1]))
-    tt = torch.tensor([x for t in tiles for x in t], dtype=torch.int32, device=dev)
+    work = torch.from_numpy(_lib.prefill_work([(0, S, 0, 0)], heads)).to(dev)
     out = torch.empty(S * heads * D, dtype=torch.float16, device=dev)
     sp = stream.cuda_stream
 
     def step(i):
-        rc = L.rh_flash_prefill(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), pos.data_ptr(), seq.data_ptr(),
-                                toff.data_ptr(), tab.data_ptr(), tt.data_ptr(), len(tiles), heads, kvh, D, bs,
-                                1.0 / math.sqrt(D), out.data_ptr(), heads * D, sp)
+        rc = L.rh_flash_prefill(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), tab.data_ptr(), work.data_ptr(),
+                                work.shape[0], heads, kvh, D, bs, 1.0 / math.sqrt(D), out.data_ptr(), heads * D, sp)
         if rc:
             raise RuntimeError(_lib.last_error())
 

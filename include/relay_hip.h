@@ -82,20 +82,31 @@ int rh_decode_chunk_keys(int head_dim);
  * that leaves CUs idle. */
 int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int max_ctx);
 
-/* Flash prefill attention for multi-token chunks: causal attention of each tile's query
- * rows against keys 0..pos of their own sequence, all read from the paged cache (a
- * chunk at an offset sees the earlier chunks' keys).
+/* Flash prefill attention for multi-token chunks: causal attention of each chunk's query
+ * rows against keys 0..pos of their own sequence, all read from the paged cache (a chunk
+ * at an offset sees the earlier chunks' keys).
  * Replaces flash_prefill_kernel<D> (cuda_kernels.cuh:37-178) and its launch
  * (cuda_backend.cu:528-545, 669-676, 689-693).
- *  tiles       int32 pairs (first token, rows), rows <= rh_prefill_tile_rows(), each
- *              tile inside one chunk (consecutive positions)
+ *  work        int32[n_work][8] records from rh_prefill_plan (16-byte aligned): one or
+ *              two blocks of rows (first row, rows, first position) and the chunk's
+ *              block-table offset
+ *  tables      the block tables the records' offsets point into
  * head_dim in {64, 128}. */
-int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool, const int* pos,
-                     const int* seq, const int* table_off, const int* tables, const int* tiles, int n_tiles,
-                     int heads, int kv_heads, int head_dim, int block_size, float scale, void* out,
-                     int64_t out_row_stride, void* stream);
+int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool, const int* tables,
+                     const int* work, int n_work, int heads, int kv_heads, int head_dim, int block_size, float scale,
+                     void* out, int64_t out_row_stride, void* stream);
 
-/* Query rows per prefill tile. */
+/* Host-side: cut the step's prefill chunks (chunk s = rows chunk_t0[s] .. +chunk_rows[s]-1
+ * of q/out at positions chunk_pos0[s].., block table at chunk_table_off[s]) into
+ * rh_flash_prefill work records: blocks of up to rh_prefill_tile_rows() rows, paired
+ * light-with-heavy when the step is large, heaviest first. Returns the record count, or a
+ * negative error code if more than `capacity` records are needed (n_chunks + rows / 128 + 1
+ * always suffice). Relay cuts the same row tiles in its launch (cuda_backend.cu:528-545),
+ * one block each, in chunk order. */
+int rh_prefill_plan(const int* chunk_t0, const int* chunk_rows, const int* chunk_pos0, const int* chunk_table_off,
+                    int n_chunks, int heads, int* work, int capacity);
+
+/* Query rows per prefill block. */
 int rh_prefill_tile_rows(void);
 
 /* Reference attention for any token (decode or prefill), any head_dim <= 256 and any

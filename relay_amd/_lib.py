@@ -50,7 +50,8 @@ SIGNATURES = {
     "rh_paged_decode_attention": (I, [P, I64, P, P, P, P, I, I, I, I, I, I, I, F, P, P, P, P, I64, P]),
     "rh_decode_chunk_keys": (I, [I]),
     "rh_decode_slice_keys": (I, [I, I, I, I, I]),
-    "rh_flash_prefill": (I, [P, I64, P, P, P, P, P, P, P, I, I, I, I, I, F, P, I64, P]),
+    "rh_flash_prefill": (I, [P, I64, P, P, P, P, I, I, I, I, I, F, P, I64, P]),
+    "rh_prefill_plan": (I, [P, P, P, P, I, I, P, I]),
     "rh_prefill_tile_rows": (I, []),
     "rh_reference_attention": (I, [P, I64, P, P, P, P, P, P, P, I, I, I, I, I, F, P, I64, P]),
     "rh_gemv_int8": (I, [P, P, I, P, P, I, I, I, F, P]),
@@ -115,3 +116,16 @@ def check(rc: int, what: str = "") -> None:
 def require_device() -> None:
     if not lib().rh_device_available():
         raise RelayHipError("no HIP device: relay_amd runs only on the GPU")
+
+
+def prefill_work(chunks, heads: int):
+    """rh_prefill_plan over chunks = [(first row, rows, first position, table offset), ...];
+    returns the int32 work records as a numpy array of shape (n_work, 8)."""
+    import numpy as np
+
+    cols = [np.ascontiguousarray([c[i] for c in chunks], dtype=np.int32) for i in range(4)]
+    cap = len(chunks) + sum(c[1] for c in chunks) // 128 + 1
+    work = np.zeros((cap, 8), dtype=np.int32)
+    n = lib().rh_prefill_plan(*[c.ctypes.data for c in cols], len(chunks), heads, work.ctypes.data, cap)
+    check(n if n < 0 else 0, "rh_prefill_plan")
+    return work[:n].copy()

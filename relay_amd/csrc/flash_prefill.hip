@@ -1,171 +1,219 @@
 // Flash prefill attention over the paged KV cache for gfx950 (fp16 MFMA, fp32 softmax).
 //
-// Work unit: one workgroup per (tile of up to 128 consecutive query rows of one chunk,
-// query head), four waves of 32 rows -- the role of relay's flash_prefill_kernel<D>
-// (cuda_kernels.cuh:28-178), re-cut for 64-wide waves and 32x32 matrix cores. The
-// workgroup walks the keys 0 .. (last row's position) 64 at a time; each 64-key tile of
-// K and V is gathered through the block table into LDS once for the four waves.
+// The role of relay's flash_prefill_kernel<D> (cuda_kernels.cuh:28-178): causal attention of
+// a chunk's query rows against keys 0 .. (row position), all read through the block table
+// (a chunk at an offset sees the earlier chunks' keys). Re-cut for 64-wide waves and 32x32
+// matrix cores:
 //
-// Per wave and 32-key sub-tile:
-//   S^T[32 keys x 32 rows] = K[32 keys x D] * Q^T[D x 32 rows]         (D/16 MFMA 32x32x16)
-//   online softmax per query row: lane = row, so the row max and sum are reductions over
-//   the lane's own 16 registers plus one swap with lane l^32
-//   O^T[D x 32 rows] += V^T[D x 32 keys] * P^T[32 keys x 32 rows]       (D/16 MFMA 32x32x16)
-// The S^T accumulators are the P^T B operands as they stand (registers 0-7 and 8-15 are
-// the two 16-key halves, in the same permuted key order the V^T A operand is read in),
-// so P never goes through LDS. The 1/sqrt(D) scale and log2(e) fold into the exp2
-// argument (one FMA per score). O^T is rescaled only when some row's maximum grew.
-//
-// LDS rows are XOR-swizzled in 16-byte chunks: K by key & 7 (the 32 keys of an A-operand
-// read spread over all banks), V by bit 2 of the key (the two key groups of a transposed
-// read land in different halves of the banks).
-//
-// Workgroups are ordered heaviest tile first, and when the head count is a multiple of 8
-// each XCD (workgroup ids are dealt round-robin over the 8 XCDs) gets a contiguous
-// range of heads, i.e. few KV heads, so its L2 holds the K/V it re-reads.
+// - Work unit: one workgroup of eight waves per (work item, query head). A work item is a
+//   block of up to 128 consecutive rows of one chunk, or a pair of blocks (i, n-1-i) of
+//   the same chunk processed one after the other, so that every workgroup does the same
+//   causal work (rh_prefill_plan makes the items; it pairs when the grid is large).
+// - Waves 2r and 2r+1 own the block's rows 32r .. 32r+31 and split every 64-key tile:
+//   keys 0-31 go to the even wave, 32-63 to the odd one. Each keeps its own running max,
+//   sum and O^T; at the end of the block the odd wave hands them to the even one through
+//   LDS. So two waves stay busy on every SIMD until the block's last tile (with one wave
+//   per 32-row strip, every SIMD drops to one wave once the short blocks finish).
+// - The workgroup walks the keys 0 .. (block's last position) 64 at a time: each tile of K
+//   and V is gathered through the block table into registers one tile ahead (its block
+//   ids another tile ahead) and written to one of two LDS buffers (one barrier per tile).
+// - Per wave and 32-key half tile:
+//     S^T[32 keys x 32 rows] = K[32 keys x D] * Q^T[D x 32 rows]        (D/16 MFMA 32x32x16)
+//     online softmax per row (lane = row): reductions over the lane's 16 registers plus
+//     one swap with lane l^32; scale and log2(e) folded into one FMA per score; the row
+//     sum from the fp16 P values with packed dot products
+//     O^T[D x 32 rows] += V^T[D x 32 keys] * P^T[32 keys x 32 rows]      (D/16 MFMA 32x32x16)
+//   The S^T accumulators are the P^T B operands as they stand. Lane (c, h) of S^T holds
+//   keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key group, so V is stored transposed with
+//   the keys of each 16-key group permuted to that order: the V^T A operand of an MFMA is
+//   one 16-byte LDS read.
+// - LDS rows are XOR-swizzled in 16-byte chunks: K by key & 7 (an A-operand read of 32
+//   keys spreads over all banks), V^T row d by (d ^ d >> 3) & 7 (the same for the V^T
+//   reads; the transposing writes, 4 bytes = 2 keys per lane, land at most 4 to a bank).
+// - When the head count is a multiple of 8, each XCD (workgroup ids are dealt round-robin
+//   over the 8 XCDs) gets a contiguous range of heads, i.e. few KV heads, so its L2 holds
+//   the K/V its workgroups re-read.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
 #include "../../include/relay_hip.h"
 #include "common.h"
 
 namespace relay_hip {
 namespace {
 
-constexpr int kRows = 128;      // query rows per workgroup
-constexpr int kWaves = 4;
+constexpr int kRows = 128;    // query rows per block
+constexpr int kWaves = 8;     // two per 32-row strip
 constexpr int kThreads = kWaves * kWave;
-constexpr int kKeyTile = 64;    // keys per LDS tile
+constexpr int kKeyTile = 64;  // keys per LDS tile
+
+// One work item: block a (t0, rows, first position), block b likewise (rows 0: none), and
+// the chunk's block-table offset. Layout of rh_prefill_plan's int32[8] records.
+struct PrefillWork {
+  int t0a, na, p0a, t0b, nb, p0b, table_off, pad;
+};
 
 struct PrefillArgs {
   const half_t* q;
   int64_t q_stride;
   const half_t* kpool;
   const half_t* vpool;
-  const int* pos;
-  const int* seq;
-  const int* table_off;
   const int* tables;
-  const int* tiles;  // (first token, rows) pairs
-  int n_tiles, heads, kv_heads, block_size, bs_shift, xcd_heads;
+  const PrefillWork* work;
+  int n_work, heads, kv_heads, block_size, bs_shift, xcd_heads;
   float scale_log2;
   half_t* out;
   int64_t out_stride;
 };
 
 __device__ __forceinline__ int kswz(int key) { return key & 7; }
-__device__ __forceinline__ int vswz(int key) { return ((key >> 2) & 1) << 2; }
+__device__ __forceinline__ int vswz(int d) { return (d ^ (d >> 3)) & 7; }
+// Position of key k (within its 16-key group) in a V^T row: lane half h reads keys
+// {4h..4h+3, 8+4h..8+4h+3} as 8 consecutive halves at 8h.
+__device__ __forceinline__ int vperm(int k) {
+  return (k & ~15) | (((k >> 2) & 1) << 3) | (((k >> 3) & 1) << 2) | (k & 3);
+}
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void flash_prefill_kernel(const PrefillArgs a) {
-  constexpr int CH = D / 8;                          // 16-byte chunks per row
-  constexpr int MK = D / 16;                         // QK MFMAs per 32-key sub-tile
-  constexpr int DT = D / 32;                         // 32-dim tiles of O^T
-  constexpr int LOADS = kKeyTile * CH / kThreads;    // 16-byte chunks per thread per tile (each of K, V)
+template <int D, bool POW2>
+__global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillArgs a) {
+  constexpr int CH = D / 8;                                 // 16-byte chunks per row
+  constexpr int MK = D / 16;                                // QK MFMAs per half tile
+  constexpr int DT = D / 32;                                // 32-dim tiles of O^T
+  constexpr int ITEMS = kKeyTile / 2 * CH;                  // (key pair, chunk) items per tile
+  constexpr int PAIRS = (ITEMS + kThreads - 1) / kThreads;  // per thread
+  constexpr int LOADS = 2 * PAIRS;                          // rows per thread per tile, each of K and V
+  constexpr int KBUF = kKeyTile * D, VBUF = D * kKeyTile;   // halves per buffer
+  constexpr int XSTRIP = DT * 16 * 64 + 2 * 64;             // floats per strip for the merge
+  constexpr int SMEM = std::max(2 * KBUF + 2 * VBUF, 2 * 4 * XSTRIP);
 
-  __shared__ __attribute__((aligned(16))) half_t sK[kKeyTile * D];
-  __shared__ __attribute__((aligned(16))) half_t sV[kKeyTile * D];
+  // Two K and two V^T buffers; reused for the merge of the half-tile partials.
+  __shared__ __attribute__((aligned(16))) half_t smem[SMEM];
+  half_t* const sK = smem;
+  half_t* const sVt = smem + 2 * KBUF;
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31, hh = lane >> 5;
+  const int strip = w >> 1, half = w & 1;
 
-  // Workgroup -> (tile, head): heaviest tiles first; per-XCD head ranges.
+  // Workgroup -> (work item, head).
   const int b = blockIdx.x;
-  int tile, head;
+  int wi, head;
   if (a.xcd_heads > 0) {
     const int xcd = b & 7, s = b >> 3;
-    tile = s / a.xcd_heads;
+    wi = s / a.xcd_heads;
     head = xcd * a.xcd_heads + s % a.xcd_heads;
   } else {
-    tile = b / a.heads;
+    wi = b / a.heads;
     head = b % a.heads;
   }
-  if (tile >= a.n_tiles) return;
-  const int t0 = a.tiles[2 * tile], nrows = a.tiles[2 * tile + 1];
+  if (wi >= a.n_work) return;
+  const PrefillWork wk = a.work[wi];
   const int kvh = head / (a.heads / a.kv_heads);
-  const int p0 = a.pos[t0];
-  const int* table = a.tables + a.table_off[a.seq[t0]];
-  const int nkeys = p0 + nrows;
+  const int* table = a.tables + wk.table_off;
   const int bs = a.block_size, sh = a.bs_shift;
-
-  // This wave's rows.
-  const int row = w * 32 + c;
-  const bool row_ok = row < nrows;
-  const bool wave_on = w * 32 < nrows;
-  const int qpos = p0 + row;
-  const int wave_last = p0 + min(w * 32 + 31, nrows - 1);
-
-  half8 qb[MK];
-#pragma unroll
-  for (int m = 0; m < MK; ++m) {
-    if (row_ok) {
-      qb[m] = load_half8(a.q + static_cast<int64_t>(t0 + row) * a.q_stride + static_cast<int64_t>(head) * D + 16 * m + 8 * hh);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qb[m][e] = 0;
-    }
-  }
-
-  float16v o[DT];
-#pragma unroll
-  for (int i = 0; i < DT; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
-  float m_run = -INFINITY, l_part = 0.0f;
   const float cl = a.scale_log2;
 
-  // Prefetch registers for one K/V tile.
+  // Block-table lookups and K/V rows in flight for the tile after the one in LDS.
+  int blk[LOADS];
   half8 kreg[LOADS], vreg[LOADS];
-  auto load_tile = [&](int k0) {
+  // Row i of this thread: key 2p + (i & 1) of the tile, 16-byte chunk cc (valid if < ITEMS).
+  auto item = [&](int i, int& kl, int& cc) {
+    const int qi = threadIdx.x + (i >> 1) * kThreads;
+    cc = qi % CH;
+    kl = 2 * (qi / CH) + (i & 1);
+    return ITEMS % kThreads == 0 || qi < ITEMS;
+  };
+
+  for (int phase = 0; phase < 2; ++phase) {
+    const int t0 = phase ? wk.t0b : wk.t0a, nrows = phase ? wk.nb : wk.na, p0 = phase ? wk.p0b : wk.p0a;
+    if (nrows <= 0) break;
+    const int nkeys = p0 + nrows;
+    const int row = strip * 32 + c;
+    const bool row_ok = row < nrows;
+    const bool wave_on = strip * 32 < nrows;
+    const int qpos = p0 + row;
+    const int wave_last = p0 + min(strip * 32 + 31, nrows - 1);  // last key any row of the strip sees
+
+    auto lookup = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int ci = threadIdx.x + i * kThreads;
-      const int kl = ci / CH, cc = ci % CH;
-      const int key = k0 + kl;
-      if (key < nkeys) {
-        const int blk = table[sh >= 0 ? key >> sh : key / bs];
-        const int slot = sh >= 0 ? key & (bs - 1) : key % bs;
-        const int64_t off = kv_row_offset(blk, a.kv_heads, kvh, bs, slot, D) + 8 * cc;
-        kreg[i] = load_half8(a.kpool + off);
-        vreg[i] = load_half8(a.vpool + off);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kreg[i][e] = 0;
-          vreg[i][e] = 0;
+      for (int i = 0; i < LOADS; ++i) {
+        int kl, cc;
+        if (item(i, kl, cc)) {
+          // Keys past the block's last are masked for every row; read a valid row instead.
+          const int key = min(k0 + kl, nkeys - 1);
+          blk[i] = table[POW2 ? key >> sh : key / bs];
         }
       }
-    }
-  };
-  auto store_tile = [&]() {
+    };
+    auto fetch = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int ci = threadIdx.x + i * kThreads;
-      const int kl = ci / CH, cc = ci % CH;
-      *reinterpret_cast<half8*>(sK + kl * D + ((cc ^ kswz(kl)) << 3)) = kreg[i];
-      *reinterpret_cast<half8*>(sV + kl * D + ((cc ^ vswz(kl)) << 3)) = vreg[i];
-    }
-  };
-
-  load_tile(0);
-  for (int k0 = 0; k0 < nkeys; k0 += kKeyTile) {
-    __syncthreads();  // the previous tile's readers are done
-    store_tile();
-    __syncthreads();
-    if (k0 + kKeyTile < nkeys) load_tile(k0 + kKeyTile);
-
+      for (int i = 0; i < LOADS; ++i) {
+        int kl, cc;
+        if (item(i, kl, cc)) {
+          const int key = min(k0 + kl, nkeys - 1);
+          const int slot = POW2 ? key & (bs - 1) : key % bs;
+          const int64_t off = kv_row_offset(blk[i], a.kv_heads, kvh, bs, slot, D) + 8 * cc;
+          kreg[i] = load_half8(a.kpool + off);
+          vreg[i] = load_half8(a.vpool + off);
+        }
+      }
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-    for (int sub = 0; sub < kKeyTile / 32; ++sub) {
-      const int kb = k0 + 32 * sub;
-      if (!wave_on || kb > wave_last) continue;  // uniform per wave
+      for (int j = 0; j < PAIRS; ++j) {
+        int kl, cc;
+        if (item(2 * j, kl, cc)) {
+          half_t* kb = sK + buf * KBUF;
+          *reinterpret_cast<half8*>(kb + kl * D + ((cc ^ kswz(kl)) << 3)) = kreg[2 * j];
+          *reinterpret_cast<half8*>(kb + (kl + 1) * D + ((cc ^ kswz(kl + 1)) << 3)) = kreg[2 * j + 1];
+          // V^T: keys kl and kl+1 are adjacent in a V^T row (vperm keeps k & 3 in place),
+          // so each of the chunk's 8 dims is one 4-byte write.
+          const int pos = vperm(kl);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int d = 8 * cc + e;
+            const half2_t v2 = {vreg[2 * j][e], vreg[2 * j + 1][e]};
+            *reinterpret_cast<half2_t*>(sVt + buf * VBUF + d * kKeyTile + (((pos >> 3) ^ vswz(d)) << 3) + (pos & 7)) =
+                v2;
+          }
+        }
+      }
+    };
+
+    half8 qb[MK];
+#pragma unroll
+    for (int m = 0; m < MK; ++m) {
+      if (row_ok) {
+        qb[m] = load_half8(a.q + static_cast<int64_t>(t0 + row) * a.q_stride + static_cast<int64_t>(head) * D +
+                           16 * m + 8 * hh);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qb[m][e] = 0;
+      }
+    }
+    float16v o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
+    float m_run = -INFINITY, l_part = 0.0f;
+
+    // This wave's 32 keys of the tile in LDS buffer `buf` starting at key k0.
+    auto compute = [&](int buf, int k0) {
+      const int kb = k0 + 32 * half;
+      if (!wave_on || kb > wave_last) return;  // uniform per wave
       float16v s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+      const half_t* kt = sK + buf * KBUF + (32 * half + c) * D;
 #pragma unroll
       for (int m = 0; m < MK; ++m) {
-        const int kl = 32 * sub + c;
-        const half8 ka = *reinterpret_cast<const half8*>(sK + kl * D + (((2 * m + hh) ^ kswz(kl)) << 3));
+        const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz(c)) << 3));
         s = mfma32x32x16(ka, qb[m], s);
       }
-      // Causal mask (and keys past the chunk, which are past every row).
-      const bool need_mask = kb + 31 > p0 + w * 32;
+      // Causal mask only where the half tile crosses a row of this strip.
+      const bool need_mask = kb + 31 > p0 + strip * 32;
       float mx = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -176,15 +224,19 @@ __global__ __launch_bounds__(kThreads, 2) void flash_prefill_kernel(const Prefil
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float base = m_new == -INFINITY ? 0.0f : m_new * cl;
-      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run * cl - base);
+      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(__builtin_fmaf(m_run, cl, -base));
       half8 pb[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pb[r >> 3][r & 7] = static_cast<half_t>(fast_exp2(__builtin_fmaf(s[r], cl, -base)));
+      // Row sum of the fp16 P values (the ones the PV product uses), fp32 accumulation.
       float psum = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(__builtin_fmaf(s[r], cl, -base));
-        psum += p;
-        pb[r >> 3][r & 7] = static_cast<half_t>(p);
-      }
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const half2_t p2 = {pb[u][e], pb[u][e + 1]};
+          psum = __builtin_amdgcn_fdot2(p2, half2_t{1.0f16, 1.0f16}, psum, false);
+        }
       l_part = l_part * alpha + psum;
       // Rescale O^T only if some row's running maximum changed.
       if (__ballot(m_new != m_run) != 0) {
@@ -195,35 +247,82 @@ __global__ __launch_bounds__(kThreads, 2) void flash_prefill_kernel(const Prefil
       }
       m_run = m_new;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 32 * dt + c;
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          half8 va;
-#pragma unroll
-          for (int sl = 0; sl < 8; ++sl) {
-            const int kl = 32 * sub + 16 * u + 8 * (sl >> 2) + 4 * hh + (sl & 3);
-            va[sl] = sV[kl * D + (((d >> 3) ^ vswz(kl)) << 3) + (d & 7)];
-          }
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d = 32 * dt + c;
+          const half8 va = *reinterpret_cast<const half8*>(sVt + buf * VBUF + d * kKeyTile +
+                                                           (((4 * half + 2 * u + hh) ^ vswz(d)) << 3));
           o[dt] = mfma32x32x16(va, pb[u], o[dt]);
         }
-      }
+    };
+
+    // Tile j lives in LDS buffer j & 1; while it is computed, tile j+1's rows are in flight
+    // into registers and tile j+2's block ids are being read.
+    const int ntiles = (nkeys + kKeyTile - 1) / kKeyTile;
+    __syncthreads();  // the previous phase's merge is done with the LDS
+    lookup(0);
+    fetch(0);
+    if (ntiles > 1) lookup(kKeyTile);
+    store(0);
+    __syncthreads();
+    if (ntiles > 1) fetch(kKeyTile);
+    if (ntiles > 2) lookup(2 * kKeyTile);
+    for (int j = 0; j < ntiles; ++j) {
+      compute(j & 1, j * kKeyTile);
+      if (j + 1 < ntiles) store((j + 1) & 1);
+      __syncthreads();
+      if (j + 2 < ntiles) fetch((j + 2) * kKeyTile);
+      if (j + 3 < ntiles) lookup((j + 3) * kKeyTile);
+    }
+
+    // Merge the strip's two halves: the odd wave's (max, sum, O^T) through LDS (the tile
+    // buffers are free after the loop's last barrier).
+    float* const xo = reinterpret_cast<float*>(smem) + strip * XSTRIP;
+    float* const xml = xo + DT * 16 * 64;
+    if (half) {
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(i * 16 + r) * 64 + lane] = o[i][r];
+      xml[lane] = m_run;
+      xml[64 + lane] = l_part;
+    }
+    __syncthreads();
+    if (!half && row_ok) {
+      // The even wave saw key 0, so its maximum is finite; the odd one's may not be.
+      const float m_b = xml[lane], l_b = xml[64 + lane];
+      const float m = fmaxf(m_run, m_b);
+      const float fa = fast_exp2((m_run - m) * cl);
+      const float fb = m_b == -INFINITY ? 0.0f : fast_exp2((m_b - m) * cl);
+      const float l = l_part * fa + l_b * fb;
+      const float inv = 1.0f / (l + __shfl_xor(l, 32));
+      half_t* orow = a.out + static_cast<int64_t>(t0 + row) * a.out_stride + static_cast<int64_t>(head) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          half4 v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * r4 + j;
+            v[j] = static_cast<half_t>((o[dt][r] * fa + xo[(dt * 16 + r) * 64 + lane] * fb) * inv);
+          }
+          *reinterpret_cast<half4*>(orow + 32 * dt + 8 * r4 + 4 * hh) = v;
+        }
     }
   }
+}
 
-  if (!row_ok) return;
-  const float l_tot = l_part + __shfl_xor(l_part, 32);
-  const float inv = 1.0f / l_tot;
-  half_t* orow = a.out + static_cast<int64_t>(t0 + row) * a.out_stride + static_cast<int64_t>(head) * D;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      half4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = static_cast<half_t>(o[dt][4 * r4 + j] * inv);
-      *reinterpret_cast<half4*>(orow + 32 * dt + 8 * r4 + 4 * hh) = v;
-    }
+template <int D>
+int launch(const PrefillArgs& a, hipStream_t s) {
+  const int grid = a.n_work * a.heads;
+  if (a.bs_shift >= 0) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, true>), dim3(grid), dim3(kThreads), 0, s, a));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, false>), dim3(grid), dim3(kThreads), 0, s, a));
+  }
+  return 0;
 }
 
 }  // namespace
@@ -233,12 +332,58 @@ using namespace relay_hip;
 
 extern "C" int rh_prefill_tile_rows(void) { return kRows; }
 
+extern "C" int rh_prefill_plan(const int* chunk_t0, const int* chunk_rows, const int* chunk_pos0,
+                               const int* chunk_table_off, int n_chunks, int heads, int* work, int capacity) {
+  RH_REQUIRE(n_chunks >= 0 && heads > 0 && capacity >= 0, "prefill plan: bad arguments");
+  long blocks = 0;
+  for (int s = 0; s < n_chunks; ++s) {
+    RH_REQUIRE(chunk_rows[s] >= 0 && chunk_pos0[s] >= 0, "prefill plan: negative rows or position");
+    blocks += (chunk_rows[s] + kRows - 1) / kRows;
+  }
+  // Pair blocks only when the unpaired grid fills the GPU (256 CUs) twice over; otherwise
+  // the halved grid would leave CUs idle.
+  const bool pair = blocks * heads >= 512;
+  std::vector<std::pair<long, PrefillWork>> items;
+  auto cost = [](int rows, int p0) { return static_cast<long>(rows) * (p0 + rows); };
+  for (int s = 0; s < n_chunks; ++s) {
+    const int n = chunk_rows[s], nb = (n + kRows - 1) / kRows;
+    auto blk = [&](int i, int& t0, int& rows, int& p0) {
+      t0 = chunk_t0[s] + i * kRows;
+      rows = std::min(kRows, n - i * kRows);
+      p0 = chunk_pos0[s] + i * kRows;
+    };
+    for (int i = 0, j = nb - 1; i <= j; ++i, --j) {
+      PrefillWork wk{};
+      wk.table_off = chunk_table_off[s];
+      blk(j, wk.t0a, wk.na, wk.p0a);  // the heavier block first
+      long c = cost(wk.na, wk.p0a);
+      if (i < j) {
+        PrefillWork light = wk;
+        blk(i, light.t0a, light.na, light.p0a);
+        if (pair) {
+          wk.t0b = light.t0a;
+          wk.nb = light.na;
+          wk.p0b = light.p0a;
+          c += cost(wk.nb, wk.p0b);
+        } else {
+          items.push_back({cost(light.na, light.p0a), light});
+        }
+      }
+      items.push_back({c, wk});
+    }
+  }
+  RH_REQUIRE(static_cast<long>(items.size()) <= capacity, "prefill plan: work capacity too small");
+  // Heaviest first: the dispatcher starts them first and the light ones fill in behind.
+  std::stable_sort(items.begin(), items.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
+  for (std::size_t i = 0; i < items.size(); ++i) std::memcpy(work + 8 * i, &items[i].second, sizeof(PrefillWork));
+  return static_cast<int>(items.size());
+}
+
 extern "C" int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
-                                const int* pos, const int* seq, const int* table_off, const int* tables,
-                                const int* tiles, int n_tiles, int heads, int kv_heads, int head_dim, int block_size,
-                                float scale, void* out, int64_t out_row_stride, void* stream) {
-  if (n_tiles == 0) return 0;
-  RH_REQUIRE(n_tiles > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "flash prefill: bad head counts");
+                                const int* tables, const int* work, int n_work, int heads, int kv_heads, int head_dim,
+                                int block_size, float scale, void* out, int64_t out_row_stride, void* stream) {
+  if (n_work == 0) return 0;
+  RH_REQUIRE(n_work > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "flash prefill: bad head counts");
   RH_REQUIRE(head_dim == 64 || head_dim == 128, "flash prefill: head_dim must be 64 or 128");
   RH_REQUIRE(block_size > 0, "flash prefill: bad block size");
   RH_REQUIRE(q_row_stride % 8 == 0 && out_row_stride % 4 == 0, "flash prefill: rows must be aligned");
@@ -251,12 +396,9 @@ extern "C" int rh_flash_prefill(const void* q, int64_t q_row_stride, const void*
   a.q_stride = q_row_stride;
   a.kpool = static_cast<const half_t*>(kpool);
   a.vpool = static_cast<const half_t*>(vpool);
-  a.pos = pos;
-  a.seq = seq;
-  a.table_off = table_off;
   a.tables = tables;
-  a.tiles = tiles;
-  a.n_tiles = n_tiles;
+  a.work = reinterpret_cast<const PrefillWork*>(work);
+  a.n_work = n_work;
   a.heads = heads;
   a.kv_heads = kv_heads;
   a.block_size = block_size;
@@ -265,12 +407,6 @@ extern "C" int rh_flash_prefill(const void* q, int64_t q_row_stride, const void*
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out = static_cast<half_t*>(out);
   a.out_stride = out_row_stride;
-  const int grid = n_tiles * heads;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 64) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL(flash_prefill_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a));
-  } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL(flash_prefill_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a));
-  }
-  return 0;
+  return head_dim == 64 ? launch<64>(a, s) : launch<128>(a, s);
 }

@@ -5,11 +5,12 @@
 // The host orchestration mirrors CudaBackend (engine/src/cuda_backend.cu:311-759) in
 // contract, not in code:
 //  - a forward pass flattens the batch (cuda_backend.cu:508-527), routes single-token
-//    chunks to the split decode kernel and longer chunks to flash prefill tiles
+//    chunks to the split decode kernel and longer chunks to flash prefill
 //    (cuda_backend.cu:528-545), runs the layers, and returns fp32 logits;
 //  - the per-step metadata goes to the device in ONE copy from a pinned buffer (the
-//    reference issues seven), and the prefill tiles are sorted heaviest first so the
-//    causal imbalance does not leave CUs idle at the end of the kernel;
+//    reference issues seven); the prefill work (rh_prefill_plan) pairs light and heavy
+//    causal row blocks and comes heaviest first, so the imbalance does not leave CUs
+//    idle at the end of the kernel;
 //  - one event per layer after its KV write backs wait_kv_written, and KV block traffic
 //    runs on a second stream under its own mutex (cuda_backend.cu:611-664).
 // Errors are C++ exceptions as in the reference: std::invalid_argument for bad batches,
@@ -346,11 +347,10 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   const int QKV = Q + 2 * c_.kv_dim();
 
   // Flatten (cuda_backend.cu:508-527).
-  std::vector<int> tok, pos, seq, table_off, tables, rows, decode, tiles;
-  std::vector<std::pair<int, int>> tile_work;  // (keys, tile index)
+  std::vector<int> tok, pos, seq, table_off, tables, rows, decode;
+  std::vector<int> pf_t0, pf_rows, pf_pos0, pf_toff;  // prefill chunks
   const int S = static_cast<int>(batch.seqs.size());
   int max_ctx = 0;
-  const int tile_rows = rh_prefill_tile_rows();
   for (int s = 0; s < S; ++s) {
     const SeqChunk& ch = batch.seqs[s];
     const int n = static_cast<int>(ch.tokens.size());
@@ -371,38 +371,36 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
       seq.push_back(s);
     }
     if (!batch.all_logits && ch.want_logits && n > 0) rows.push_back(t0 + n - 1);
-    // Routing: one token -> decode; more -> prefill tiles.
+    // Routing: one token -> decode; more -> prefill.
     if (n == 1) {
       // (token row, context length, block-table offset): the decode kernel's descriptor
       decode.insert(decode.end(), {t0, end, table_off.back(), 0});
       max_ctx = std::max(max_ctx, end);
     } else {
-      for (int r = 0; r < n; r += tile_rows) {
-        const int nr = std::min(tile_rows, n - r);
-        tile_work.push_back({ch.start_pos + r + nr, static_cast<int>(tiles.size() / 2)});
-        tiles.push_back(t0 + r);
-        tiles.push_back(nr);
-      }
+      pf_t0.push_back(t0);
+      pf_rows.push_back(n);
+      pf_pos0.push_back(ch.start_pos);
+      pf_toff.push_back(table_off.back());
     }
   }
   const int T = static_cast<int>(tok.size()), R = static_cast<int>(rows.size());
   if (T == 0) return {};
   if (T > max_tokens_) throw std::invalid_argument("batch has more tokens than max_batch_tokens");
-  // Heaviest prefill tile first.
-  std::stable_sort(tile_work.begin(), tile_work.end(), [](auto& a, auto& b) { return a.first > b.first; });
-  std::vector<int> sorted_tiles;
-  sorted_tiles.reserve(tiles.size());
-  for (auto& tw : tile_work) {
-    sorted_tiles.push_back(tiles[2 * tw.second]);
-    sorted_tiles.push_back(tiles[2 * tw.second + 1]);
-  }
-  const int n_dec = static_cast<int>(decode.size() / 4), n_tiles = static_cast<int>(sorted_tiles.size() / 2);
+  // Prefill work records (heaviest first).
+  const int n_chunks = static_cast<int>(pf_t0.size());
+  std::vector<int> work(8 * static_cast<std::size_t>(n_chunks + T / 128 + 1));
+  const int n_work = n_chunks ? rh_prefill_plan(pf_t0.data(), pf_rows.data(), pf_pos0.data(), pf_toff.data(), n_chunks,
+                                                c_.heads, work.data(), static_cast<int>(work.size() / 8))
+                              : 0;
+  if (n_work < 0) throw std::runtime_error(std::string("HIP: ") + rh_last_error());
+  work.resize(8 * static_cast<std::size_t>(n_work));
+  const int n_dec = static_cast<int>(decode.size() / 4);
 
   // One packed metadata copy.
-  // The decode descriptors come first: 16-byte aligned.
-  const std::size_t o_dec = 0, o_tok = o_dec + decode.size(), o_pos = o_tok + T, o_seq = o_pos + T,
-                    o_toff = o_seq + T, o_tab = o_toff + S, o_rows = o_tab + tables.size(), o_tiles = o_rows + R,
-                    total = o_tiles + sorted_tiles.size();
+  // The decode descriptors and prefill work records come first: 16-byte aligned.
+  const std::size_t o_dec = 0, o_work = o_dec + decode.size(), o_tok = o_work + work.size(), o_pos = o_tok + T,
+                    o_seq = o_pos + T, o_toff = o_seq + T, o_tab = o_toff + S, o_rows = o_tab + tables.size(),
+                    total = o_rows + R;
   meta_host_.reserve(total * sizeof(int));
   int* mh = static_cast<int*>(meta_host_.p);
   auto put = [&](std::size_t off, const std::vector<int>& v) { std::copy(v.begin(), v.end(), mh + off); };
@@ -413,7 +411,7 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   put(o_tab, tables);
   put(o_rows, rows);
   put(o_dec, decode);
-  put(o_tiles, sorted_tiles);
+  put(o_work, work);
   if (meta_dev_.n < total) meta_dev_ = DeviceArray<int>(total * 2);
   HIP_CHECK(hipMemcpyAsync(meta_dev_.p, mh, total * sizeof(int), hipMemcpyHostToDevice, stream_));
   const int* d_tok = meta_dev_.p + o_tok;
@@ -423,7 +421,7 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   const int* d_tab = meta_dev_.p + o_tab;
   const int* d_rows = meta_dev_.p + o_rows;
   const int* d_dec = meta_dev_.p + o_dec;
-  const int* d_tiles = meta_dev_.p + o_tiles;
+  const int* d_work = meta_dev_.p + o_work;
 
   // Keys per decode split: relay fixes 512 (cuda_kernels.cuh:190); here the planner picks
   // the split for this step's shape (results differ only by rounding).
@@ -457,9 +455,9 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
     if (observer) observer->kv_written(l);
     if (fast_attention_) {
-      if (n_tiles)
-        RH_CHECK(rh_flash_prefill(qh_.p, Q, kc, vc, d_pos, d_seq, d_toff, d_tab, d_tiles, n_tiles, c_.heads,
-                                  c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
+      if (n_work)
+        RH_CHECK(rh_flash_prefill(qh_.p, Q, kc, vc, d_tab, d_work, n_work, c_.heads, c_.kv_heads, D,
+                                  layout_.block_size, scale, attn_.p, Q, stream_));
       if (n_dec)
         RH_CHECK(rh_paged_decode_attention(qh_.p, Q, kc, vc, d_dec, d_tab, n_dec, c_.heads,
                                            c_.kv_heads, D, layout_.block_size, slice, parts, scale,

@@ -57,8 +57,7 @@ def test_kernel_launchers_validate_shapes_before_launching():
     lib = _lib.lib()
     assert lib.rh_gemv_int8(None, None, 0, None, None, 0, 64, 64, 0.0, None) != 0
     assert "T must be" in _lib.last_error()
-    assert lib.rh_flash_prefill(None, 64, None, None, None, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64,
-                                None) != 0
+    assert lib.rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64, None) != 0
     assert lib.rh_prefill_tile_rows() == 128
     assert lib.rh_gemv_int8_max_tokens() == 16
 
@@ -94,3 +93,41 @@ def test_llama3_config_matches_the_stated_shape():
     c = llama3_8b()
     assert (c.hidden, c.layers, c.heads, c.kv_heads, c.head_dim, c.intermediate, c.vocab) == \
         (4096, 32, 32, 8, 128, 14336, 128256)
+
+
+@pytest.mark.parametrize("heads", [4, 32])
+def test_prefill_plan_covers_every_row_once(heads):
+    """rh_prefill_plan (host code): every row of every chunk in exactly one block of at
+    most rh_prefill_tile_rows() rows, blocks inside their chunk with the chunk's positions
+    and table, records heaviest first; a large step pairs light with heavy blocks."""
+    rows = _lib.lib().rh_prefill_tile_rows()
+    chunks = [(0, 2048, 0, 0), (2048, 300, 700, 130), (2348, 2, 5, 200), (2350, 129, 0, 210)]
+    work = _lib.prefill_work(chunks, heads)
+    seen, cost = [], []
+    for rec in work:
+        c = 0
+        for t0, n, p0 in (rec[0:3], rec[3:6]):
+            if n == 0:
+                continue
+            assert 0 < n <= rows
+            ch = [x for x in chunks if x[0] <= t0 < x[0] + x[1]]
+            assert len(ch) == 1 and t0 + n <= ch[0][0] + ch[0][1] and rec[6] == ch[0][3]
+            assert p0 == ch[0][2] + (t0 - ch[0][0])
+            seen.extend(range(t0, t0 + n))
+            c += int(n) * int(p0 + n)
+        cost.append(c)
+    assert sorted(seen) == list(range(2479))
+    assert cost == sorted(cost, reverse=True)
+    paired = sum(1 for rec in work if rec[4] > 0)
+    assert (paired > 0) == (heads == 32)
+
+
+def test_prefill_plan_rejects_small_capacity():
+    import numpy as np
+
+    a = np.array([0], np.int32)
+    n = np.array([1000], np.int32)
+    work = np.zeros((1, 8), np.int32)
+    assert _lib.lib().rh_prefill_plan(a.ctypes.data, n.ctypes.data, a.ctypes.data, a.ctypes.data, 1, 4,
+                                      work.ctypes.data, 1) < 0
+    assert "capacity" in _lib.last_error()

@@ -16,15 +16,15 @@ from helpers import PagedCase, bits_to_f32, f16_bits
 pytestmark = pytest.mark.gpu
 
 
-def tiles_of(case, rows):
-    tiles, t = [], 0
+def chunks_of(case):
+    """(first row, rows, first position, table offset) of each chunk of the case."""
+    chunks, t = [], 0
     for s in range(len(case.table_off)):
         n = case.seq.count(s)
-        for r in range(0, n, rows):
-            tiles.append((t + r, min(rows, n - r)))
+        if n:
+            chunks.append((t, n, case.pos[t], case.table_off[s]))
         t += n
-    tiles.sort(key=lambda x: -(case.pos[x[0]] + x[1]))
-    return tiles
+    return chunks
 
 
 def run_prefill(torch, dev, case):
@@ -33,13 +33,12 @@ def run_prefill(torch, dev, case):
     L = _lib.lib()
     d = case.to_device(torch, dev)
     H, KVH, D = case.heads, case.kv_heads, case.D
-    tiles = tiles_of(case, L.rh_prefill_tile_rows())
-    tt = torch.tensor([v for tl in tiles for v in tl], dtype=torch.int32, device=dev)
+    work = torch.from_numpy(_lib.prefill_work(chunks_of(case), H)).to(dev)
     out = torch.full((case.T, H * D), float("nan"), dtype=torch.float16, device=dev)
-    print(f"prefill case: T={case.T} tiles={len(tiles)} H={H} KVH={KVH} D={D} bs={case.bs}", flush=True)
-    rc = L.rh_flash_prefill(d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), d["pos"].data_ptr(),
-                            d["seq"].data_ptr(), d["table_off"].data_ptr(), d["tables"].data_ptr(), tt.data_ptr(),
-                            len(tiles), H, KVH, D, case.bs, 1.0 / math.sqrt(D), out.data_ptr(), H * D, None)
+    print(f"prefill case: T={case.T} work={work.shape[0]} H={H} KVH={KVH} D={D} bs={case.bs}", flush=True)
+    rc = L.rh_flash_prefill(d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), d["tables"].data_ptr(),
+                            work.data_ptr(), work.shape[0], H, KVH, D, case.bs, 1.0 / math.sqrt(D), out.data_ptr(),
+                            H * D, None)
     _lib.check(rc, "rh_flash_prefill")
     torch.cuda.synchronize()
     return out.cpu().numpy().astype(np.float32)
@@ -98,6 +97,14 @@ def test_config3_shape(torch_mod, dev):
     check_close(run_prefill(torch_mod, dev, case), oracle_out(case))
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_paired_blocks(torch_mod, dev, D):
+    """A step large enough that rh_prefill_plan pairs light and heavy blocks: an odd block
+    count, a chunk at an offset, a ragged last block."""
+    case = PagedCase([1300, 900, 40], [1300, 700, 40], 32, 4, D, 16, seed=D + 1)
+    check_close(run_prefill(torch_mod, dev, case), oracle_out(case))
+
+
 def test_gather_is_bit_exact_under_permutation(torch_mod, dev):
     case = PagedCase([400], [400], 8, 2, 64, 16, seed=1)
     a = run_prefill(torch_mod, dev, case)
@@ -125,6 +132,5 @@ def test_reference_kernel_matches_oracle(torch_mod, dev, D):
 def test_rejects_unsupported_head_dim(torch_mod, dev):
     from relay_amd import _lib
 
-    rc = _lib.lib().rh_flash_prefill(None, 64, None, None, None, None, None, None, None, 1, 4, 4, 32, 16, 0.1, None,
-                                     64, None)
+    rc = _lib.lib().rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 4, 32, 16, 0.1, None, 64, None)
     assert rc != 0 and "head_dim" in _lib.last_error()
