@@ -11,9 +11,11 @@ greedy steps. tests/golden/make_goldens.py runs it on the reference's own CPU ba
 The CPU oracle must reproduce every row bit for bit (test_oracle.py); the GPU backend must
 give the same tokens with every row within 2e-3 of the oracle's (test_e2e.py).
 
-Weights: relay_amd.model.HostWeights.synthetic (counter-based N(0, 0.02), norms 1), seed 0.
-Scaled variants keep the full layer shapes (hidden, heads, head_dim, intermediate, vocab)
-and cut the layer count and context, as the configs allow for CPU runs.
+Weights: relay_amd.model.HostWeights.synthetic (counter-based N(0, 0.02), norms 1), seed 0;
+fp32 for config 1, rounded to fp16 values (RNE) for the shapes of configs 3 and 5, whose
+models are specified with fp16 weights. Scaled variants keep the full layer shapes (hidden,
+heads, head_dim, intermediate, vocab) and cut the layer count and context, as the configs
+allow for CPU runs.
 """
 from __future__ import annotations
 
@@ -33,6 +35,7 @@ GOLDENS = {
     # Config 5's shape (D 128, 32/8 heads, llama3 RoPE scaling), 2 layers, 128-token prompt.
     "llama3_8b_2layer": (dataclasses.replace(llama3_8b(), layers=2), 128, 8),
 }
+FP16_WEIGHTS = {"tinyllama_2layer", "llama3_8b_2layer"}
 
 BLOCK_SIZE = 16
 MAX_BATCH_TOKENS = 2048  # the whole prompt is one chunk
@@ -47,8 +50,22 @@ def prompt_of(name: str) -> list:
     return np.random.default_rng(0).integers(0, c.vocab, size=n).astype(np.int32).tolist()
 
 
+def _to_f16_values(a):
+    if a is None:
+        return None
+    np.copyto(a, a.astype(np.float16).astype(np.float32))  # RNE, in place
+    return a
+
+
 def weights_for(name: str) -> HostWeights:
-    return HostWeights.synthetic(config_of(name), seed=0)
+    w = HostWeights.synthetic(config_of(name), seed=0)
+    if name in FP16_WEIGHTS:
+        for t in (w.embed, w.lm_head, w.final_norm):
+            _to_f16_values(t)
+        for L in w.layers:
+            for f in ("attn_norm", "wqkv", "bqkv", "wo", "mlp_norm", "w_gate_up", "w_down"):
+                _to_f16_values(getattr(L, f))
+    return w
 
 
 def num_blocks(name: str) -> int:
