@@ -13,8 +13,10 @@ Cache cannot hold the working set between launches.
 
 Also reported in the same line: flash prefill attention TFLOP/s (config 3's 2048-token
 prompt, 32 / 4 heads, D 64, causal), int8 GEMV GB/s at Llama-3-8B shapes (config 4),
-TinyLlama-1.1B decode tok/s at 32 x 2048 (config 3b, whole forward pass), and the CPU
-oracle's attention on a bounded sample of config 2 (cpu_baseline).
+TinyLlama-1.1B decode tok/s at 32 x 2048 (config 3b, whole forward pass), config 1's
+SmolLM2-135M 512-token prompt + 128 greedy steps (tok/s), config 5's Llama-3-8B mixed
+step (48 decode sequences at 8192 + one 512-token chunk; fp16 and int8 weights), and the
+CPU oracle's attention on a bounded sample of config 2 (cpu_baseline).
 """
 from __future__ import annotations
 
@@ -212,6 +214,74 @@ def bench_tinyllama_decode(steps, int8=False, n_seq=32, ctx=2048):
     return {"ms_wall": round(wall, 3), "ms_device": round(dev_ms, 3), "tok_s": round(n_seq / wall * 1e3, 1)}
 
 
+# ---- config 1: SmolLM2-135M, 512-token prompt + 128 greedy steps --------------------------
+
+def bench_config1(prompt_len=512, new_tokens=128):
+    """Greedy generation through relay's batch composition (relay_amd.engine.GreedyEngine)
+    on the HIP backend with synthetic device weights; wall clock including the host loop
+    (logits to the host, argmax) as relay-generate measures it (relay_generate.cpp:61-96)."""
+    from relay_amd import HipBackend, HipOptions, smollm2_135m
+    from relay_amd.engine import GreedyEngine
+
+    c = smollm2_135m()
+    bs = 16
+    nb = (prompt_len + new_tokens) // bs + 2
+    be = HipBackend(None, nb, bs, max_batch_tokens=2048, options=HipOptions(False, False), config=c,
+                    synthetic_seed=0, synthetic_std=0.02)
+    prompt = np.random.default_rng(0).integers(0, c.vocab, size=prompt_len).tolist()
+    marks = []
+    runs = []
+    for rep in range(3):  # the first run warms up
+        marks.clear()
+        eng = GreedyEngine(be, nb, bs, 2048, 8, on_logits=lambda rid, i, row: marks.append(time.perf_counter()))
+        eng.add(1, prompt, new_tokens)
+        t0 = time.perf_counter()
+        out = eng.run_all()[1]
+        t1 = time.perf_counter()
+        assert len(out) == new_tokens
+        runs.append((marks[0] - t0, t1 - marks[0], t1 - t0))
+    be.close()
+    prefill, decode, total = (float(np.median([r[i] for r in runs[1:]])) for i in range(3))
+    return {"prompt_ms": round(prefill * 1e3, 2), "decode_tok_s": round((new_tokens - 1) / decode, 1),
+            "total_s": round(total, 4), "gen_tok_s": round(new_tokens / total, 1)}
+
+
+# ---- config 5: Llama-3-8B mixed step ------------------------------------------------------
+
+def bench_llama3_mixed(steps, int8=False, n_dec=48, ctx=8192, chunk=512):
+    """One forward step: n_dec decode sequences at context ctx plus one chunk-token prefill
+    chunk at position 0, synthetic fp16 (or int8) device weights and a random KV cache."""
+    from relay_amd import HipBackend, HipOptions, llama3_8b
+    from relay_amd.backend import ForwardBatch, SeqChunk
+
+    c = llama3_8b()
+    bs = 16
+    per = (ctx + bs) // bs + 1
+    nb = n_dec * per + chunk // bs + 1
+    be = HipBackend(None, nb, bs, max_batch_tokens=n_dec + chunk, max_context=per * bs,
+                    options=HipOptions(False, int8), config=c, synthetic_seed=0, synthetic_std=0.02)
+    be.fill_kv_random(seed=5, std=1.0)
+    rng = np.random.default_rng(1)
+    ptable = list(range(n_dec * per, n_dec * per + chunk // bs))
+    times = []
+    for r in range(steps + 2):
+        seqs = [SeqChunk([int(rng.integers(c.vocab))], ctx - 1, list(range(i * per, (i + 1) * per)), True)
+                for i in range(n_dec)]
+        seqs.append(SeqChunk(rng.integers(0, c.vocab, size=chunk).tolist(), 0, ptable, True))
+        t0 = time.perf_counter()
+        be.forward(ForwardBatch(seqs))
+        wall = (time.perf_counter() - t0) * 1e3
+        if r >= 2:
+            times.append((wall, be.last_forward_ms()))
+    be.close()
+    wall = float(np.median([t[0] for t in times]))
+    dev_ms = float(np.median([t[1] for t in times]))
+    kv = 2 * n_dec * ctx * c.kv_heads * c.head_dim * 2 * c.layers
+    roof_ms = (kv + (8.0e9 if int8 else 15.0e9)) / HBM_PEAK_GBS / 1e6
+    return {"ms_wall": round(wall, 3), "ms_device": round(dev_ms, 3), "decode_tok_s": round(n_dec / wall * 1e3, 1),
+            "roofline_ms": round(roof_ms, 2), "frac_roofline": round(roof_ms / dev_ms, 4)}
+
+
 # ---- CPU baseline ----------------------------------------------------------------------
 
 def cpu_baseline(sample_seqs=8, ctx=2048, heads=32, kvh=4, D=64, bs=16):
@@ -307,6 +377,13 @@ def main():
         extra["tinyllama_decode_32x2048"] = td
         td8 = bench_tinyllama_decode(10, int8=True)
         extra["tinyllama_decode_32x2048_int8"] = td8
+        c1 = bench_config1()
+        log(f"config 1 (SmolLM2 512 + 128 greedy): {c1}")
+        extra["smollm2_512_plus_128_greedy"] = c1
+        for int8 in (False, True):
+            l3 = bench_llama3_mixed(5, int8=int8)
+            log(f"llama3-8b mixed step (48 x 8192 decode + 512 chunk){' int8' if int8 else ''}: {l3}")
+            extra["llama3_8b_mixed_step" + ("_int8" if int8 else "")] = l3
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
