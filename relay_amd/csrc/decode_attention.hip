@@ -2,10 +2,11 @@
 //
 // Work unit: one workgroup per (decode token, kv head, 16-head chunk of its query group,
 // slice of `slice_keys` context keys) -- the split of relay's decode_attention_kernel
-// (cuda_kernels.cuh:180-339). The slice is cut into chunks of 32 KB of K+V (128 keys at
-// head_dim 64, 64 at 128) dealt round-robin to the workgroup's 4 or 8 waves. Per chunk a
-// wave issues every K and V load first (32 KB in flight per wave, ~256 KB per CU), then
-// walks the chunk in steps of 32 keys:
+// (cuda_kernels.cuh:180-339). The slice is cut into chunks of 16 KB of K+V (64 keys at
+// head_dim 64, 32 at 128) dealt round-robin to the workgroup's 4 or 8 waves. Per chunk a
+// wave issues every K and V load first (16 KB in flight per wave, 128 KB per 8-wave
+// workgroup), then walks the chunk in steps of 32 keys (measured: 16 KB chunks stream
+// faster than 32 KB ones, whose registers also cap a CU at 8 waves):
 //
 //   S^T[16 keys x 16 heads] = K[16 keys x D] * Q^T[D x 16 heads]     (MFMA 16x16x32, D/32 per tile)
 //   online softmax per head in the log2 domain, per lane (lane = head column)
@@ -75,7 +76,7 @@ __device__ __forceinline__ int vswz(int key) { return ((key >> 2) & 3) << 1; }
 
 template <int D>
 constexpr int stage_keys() {
-  return D == 64 ? 128 : 64;
+  return D == 64 ? 64 : 32;
 }
 
 // One chunk of a wave's K and V in registers.
