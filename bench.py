@@ -163,8 +163,9 @@ def bench_gemv(torch, dev, stream, steps, warmup, Ts=(1, 4, 8)):
         wbytes = N * K
         copies = max(2, math.ceil(1.5 * MALL_BYTES / wbytes) + 1)
         ws = []
+        ldw = L.rh_gemv_int8_row_stride(K)  # the backend's int8 layout
         for c in range(copies):
-            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            w = torch.randint(-127, 128, (N, ldw), dtype=torch.int8, device=dev)
             s = (torch.rand(N, device=dev) * 0.019 + 0.001).half()
             ws.append((w, s))
         for T in Ts:
@@ -173,7 +174,7 @@ def bench_gemv(torch, dev, stream, steps, warmup, Ts=(1, 4, 8)):
 
             def step(i):
                 w, s = ws[i % copies]
-                rc = L.rh_gemv_int8(w.data_ptr(), s.data_ptr(), 1, x.data_ptr(), y.data_ptr(), T, K, N, 0.0, sp)
+                rc = L.rh_gemv_int8(w.data_ptr(), ldw, s.data_ptr(), 1, x.data_ptr(), y.data_ptr(), T, K, N, 0.0, sp)
                 if rc:
                     raise RuntimeError(_lib.last_error())
 

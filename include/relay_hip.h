@@ -123,25 +123,33 @@ int rh_reference_attention(const float* q, int64_t q_row_stride, const void* kpo
 /* ---- weight-only int8 ----------------------------------------------------------- */
 
 /* y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for
- * 1 <= T <= 16 tokens. W8 int8 [N, K] row-major; x fp16 [T, K]; y fp32 [T, N].
+ * 1 <= T <= 16 tokens. W8 int8 [N, K] rows ldw bytes apart (ldw >= K, a multiple of 16;
+ * relay's layout is ldw = K); x fp16 [T, K]; y fp32 [T, N].
  * scale is fp32 [N] (scale_is_f16 = 0, relay's quantizer) or fp16 [N] (scale_is_f16 = 1).
  * K must be a multiple of 16 and W8 / x 16-byte aligned.
  * Replaces gemv_int8_kernel<8> (cuda_kernels.cuh:378-430) and its dispatch
  * (cuda_backend.cu:711-718). */
-int rh_gemv_int8(const int8_t* w8, const void* scale, int scale_is_f16, const void* x, float* y, int T, int K,
-                 int N, float beta, void* stream);
+int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x, float* y,
+                 int T, int K, int N, float beta, void* stream);
+
+/* The row stride (bytes) rh_gemv_int8 streams fastest for rows of K int8 values: K rounded
+ * up to 16, plus 256 when that is a multiple of 2048 (rows a power-of-two multiple of 2 KB
+ * apart put every load of a 16-row tile on the same HBM channels). No counterpart in
+ * relay, whose int8 matrices are dense (cuda_backend.cu:282-304). */
+int64_t rh_gemv_int8_row_stride(int K);
 
 /* Largest T rh_gemv_int8 takes. */
 int rh_gemv_int8_max_tokens(void);
 
 /* Per-row symmetric int8 quantization of an fp32 matrix [N, K] on the device:
- * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale).
+ * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale),
+ * q rows ldq bytes apart (ldq >= K; the bytes past K are not written).
  * Same values as the reference's host quantizer (cuda_backend.cu:282-304). */
-int rh_quantize_int8(const float* w, int N, int K, int8_t* q, float* scale, void* stream);
+int rh_quantize_int8(const float* w, int N, int K, int8_t* q, int64_t ldq, float* scale, void* stream);
 
-/* W16[i] = fp16(W8[i] * scale[i / K]) for a whole [N, K] matrix (the T > 16 path).
- * Replaces dequant_int8_kernel (cuda_kernels.cuh:432-436). */
-int rh_dequant_int8(const int8_t* w8, const float* scale, int N, int K, void* w16, void* stream);
+/* W16[n, k] = fp16(W8[n, k] * scale[n]) for a whole [N, K] matrix (W8 rows ldw bytes apart,
+ * W16 dense), the T > 16 path. Replaces dequant_int8_kernel (cuda_kernels.cuh:432-436). */
+int rh_dequant_int8(const int8_t* w8, int64_t ldw, const float* scale, int N, int K, void* w16, void* stream);
 
 /* ---- the rest of a transformer layer ------------------------------------------------ */
 

@@ -54,10 +54,11 @@ SIGNATURES = {
     "rh_prefill_plan": (I, [P, P, P, P, I, I, P, I]),
     "rh_prefill_tile_rows": (I, []),
     "rh_reference_attention": (I, [P, I64, P, P, P, P, P, P, P, I, I, I, I, I, F, P, I64, P]),
-    "rh_gemv_int8": (I, [P, P, I, P, P, I, I, I, F, P]),
+    "rh_gemv_int8": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
+    "rh_gemv_int8_row_stride": (I64, [I]),
     "rh_gemv_int8_max_tokens": (I, []),
-    "rh_quantize_int8": (I, [P, I, I, P, P, P]),
-    "rh_dequant_int8": (I, [P, P, I, I, P, P]),
+    "rh_quantize_int8": (I, [P, I, I, P, I64, P, P]),
+    "rh_dequant_int8": (I, [P, I64, P, I, I, P, P]),
     "rh_f32_to_f16": (I, [P, P, SZ, P]),
     "rh_embed": (I, [P, I, P, I, P, P]),
     "rh_rmsnorm": (I, [P, P, I, P, I, F, P, P]),

@@ -54,9 +54,11 @@ using relay_hip_host::PinnedBuffer;
       throw std::runtime_error(std::string("rocBLAS: ") + rocblas_status_to_string(_s) + " at " #x); \
   } while (0)
 
-// A weight matrix [N, K]: fp16, or int8 with one fp32 scale per row.
+// A weight matrix [N, K]: fp16, or int8 with one fp32 scale per row (int8 rows ldw bytes
+// apart, rh_gemv_int8_row_stride).
 struct DeviceMatrix {
   int N = 0, K = 0;
+  std::int64_t ldw = 0;
   DeviceArray<std::uint16_t> f16;
   DeviceArray<std::int8_t> i8;
   DeviceArray<float> scale;
@@ -273,7 +275,8 @@ DeviceMatrix HipBackend::make_matrix(const float* host, int N, int K, const Weig
     m.f16 = make_f16(host, n, src, stream_id);
     return m;
   }
-  m.i8 = DeviceArray<std::int8_t>(n);
+  m.ldw = rh_gemv_int8_row_stride(K);
+  m.i8 = DeviceArray<std::int8_t>(static_cast<std::size_t>(N) * static_cast<std::size_t>(m.ldw));
   m.scale = DeviceArray<float>(N);
   if (src.synthetic) {
     // fp32 rows drawn on the device, then the same quantizer as the host-weight path.
@@ -283,11 +286,13 @@ DeviceMatrix HipBackend::make_matrix(const float* host, int N, int K, const Weig
       const int rows = std::min<int>(static_cast<int>(rows_per), N - r0);
       RH_CHECK(rh_fill_normal_f32(stage_.p, static_cast<std::size_t>(rows) * K, src.seed, stream_id * 65536 + r0, 0.0f,
                                   src.std, stream_));
-      RH_CHECK(rh_quantize_int8(stage_.p, rows, K, m.i8.p + static_cast<std::size_t>(r0) * K, m.scale.p + r0, stream_));
+      RH_CHECK(rh_quantize_int8(stage_.p, rows, K, m.i8.p + static_cast<std::size_t>(r0) * m.ldw, m.ldw,
+                                m.scale.p + r0, stream_));
     }
   } else {
     upload_f32_rows(host, N, K, [&](const float* chunk, int r0, int rows) {
-      RH_CHECK(rh_quantize_int8(chunk, rows, K, m.i8.p + static_cast<std::size_t>(r0) * K, m.scale.p + r0, stream_));
+      RH_CHECK(rh_quantize_int8(chunk, rows, K, m.i8.p + static_cast<std::size_t>(r0) * m.ldw, m.ldw,
+                                m.scale.p + r0, stream_));
     });
   }
   dequant_elems_ = std::max(dequant_elems_, n);
@@ -334,10 +339,10 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
   if (T <= rh_gemv_int8_max_tokens()) {
-    RH_CHECK(rh_gemv_int8(W.i8.p, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
+    RH_CHECK(rh_gemv_int8(W.i8.p, W.ldw, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
     return;
   }
-  RH_CHECK(rh_dequant_int8(W.i8.p, W.scale.p, W.N, W.K, dequant_.p, stream_));
+  RH_CHECK(rh_dequant_int8(W.i8.p, W.ldw, W.scale.p, W.N, W.K, dequant_.p, stream_));
   gemm_f16(dequant_.p, x, y, T, W.K, W.N, beta);
 }
 

@@ -129,7 +129,7 @@ __global__ void kv_scatter_kernel(uint4v* k, uint4v* v, const int* blocks, int n
 }
 
 // One wave per row: scale = max|w| / 127 (1 for a zero row), q = rint(w / scale).
-__global__ void quantize_int8_kernel(const float* w, int N, int K, int8_t* q, float* scale) {
+__global__ void quantize_int8_kernel(const float* w, int N, int K, int8_t* q, int64_t ldq, float* scale) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -139,13 +139,16 @@ __global__ void quantize_int8_kernel(const float* w, int N, int K, int8_t* q, fl
   mx = wave_max(mx);
   const float s = mx > 0.0f ? mx / 127.0f : 1.0f;
   if (lane == 0) scale[n] = s;
-  for (int k = lane; k < K; k += 64) q[static_cast<int64_t>(n) * K + k] = static_cast<int8_t>(rintf(row[k] / s));
+  for (int k = lane; k < K; k += 64) q[static_cast<int64_t>(n) * ldq + k] = static_cast<int8_t>(rintf(row[k] / s));
 }
 
-__global__ void dequant_int8_kernel(const int8_t* w8, const float* scale, int K, int64_t total, half_t* out) {
+__global__ void dequant_int8_kernel(const int8_t* w8, int64_t ldw, const float* scale, int K, int64_t total,
+                                    half_t* out) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    out[i] = static_cast<half_t>(static_cast<float>(w8[i]) * scale[i / K]);
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t n = i / K;
+    out[i] = static_cast<half_t>(static_cast<float>(w8[n * ldw + (i - n * K)]) * scale[n]);
+  }
 }
 
 // splitmix64 finalizer (Vigna), the mixing function of the synthetic-input generator.
@@ -300,18 +303,19 @@ int rh_kv_scatter(void* kpool, void* vpool, const int* blocks, int n, size_t blo
   return 0;
 }
 
-int rh_quantize_int8(const float* w, int N, int K, int8_t* q, float* scale, void* stream) {
-  RH_REQUIRE(N > 0 && K > 0, "quantize_int8: bad shape");
+int rh_quantize_int8(const float* w, int N, int K, int8_t* q, int64_t ldq, float* scale, void* stream) {
+  RH_REQUIRE(N > 0 && K > 0 && ldq >= K, "quantize_int8: bad shape");
   RH_TRY_LAUNCH(hipLaunchKernelGGL(quantize_int8_kernel, dim3((N + 3) / 4), dim3(kThreads), 0,
-                                   static_cast<hipStream_t>(stream), w, N, K, q, scale));
+                                   static_cast<hipStream_t>(stream), w, N, K, q, ldq, scale));
   return 0;
 }
 
-int rh_dequant_int8(const int8_t* w8, const float* scale, int N, int K, void* w16, void* stream) {
-  RH_REQUIRE(N > 0 && K > 0, "dequant_int8: bad shape");
+int rh_dequant_int8(const int8_t* w8, int64_t ldw, const float* scale, int N, int K, void* w16, void* stream) {
+  RH_REQUIRE(N > 0 && K > 0 && ldw >= K, "dequant_int8: bad shape");
   const int64_t total = static_cast<int64_t>(N) * K;
   RH_TRY_LAUNCH(hipLaunchKernelGGL(dequant_int8_kernel, dim3(grid_for(total)), dim3(kThreads), 0,
-                                   static_cast<hipStream_t>(stream), w8, scale, K, total, static_cast<half_t*>(w16)));
+                                   static_cast<hipStream_t>(stream), w8, ldw, scale, K, total,
+                                   static_cast<half_t*>(w16)));
   return 0;
 }
 

@@ -16,21 +16,25 @@ pytestmark = pytest.mark.gpu
 EPS32 = 2.0 ** -24
 
 
-def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False):
+def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
+    """ldw None: relay's dense rows; otherwise rows ldw bytes apart with junk in the padding."""
     from relay_amd import _lib
 
     N, K = w8.shape
     T = x_bits.shape[0]
-    W = torch.from_numpy(w8).to(dev)
+    ldw = K if ldw is None else ldw
+    padded = np.full((N, ldw), 0x7F, np.int8)
+    padded[:, :K] = w8
+    W = torch.from_numpy(padded).to(dev)
     if f16_scale:
         S = torch.from_numpy(f16_bits(scale).view(np.int16)).to(dev)
     else:
         S = torch.from_numpy(scale.astype(np.float32)).to(dev)
     X = torch.from_numpy(x_bits.view(np.int16)).to(dev)
     Y = torch.from_numpy(y0.copy()).to(dev) if y0 is not None else torch.full((T, N), float("nan"), device=dev)
-    print(f"gemv case: T={T} K={K} N={N} beta={beta} f16_scale={f16_scale}", flush=True)
-    rc = _lib.lib().rh_gemv_int8(W.data_ptr(), S.data_ptr(), int(f16_scale), X.data_ptr(), Y.data_ptr(), T, K, N,
-                                 beta, None)
+    print(f"gemv case: T={T} K={K} N={N} ldw={ldw} beta={beta} f16_scale={f16_scale}", flush=True)
+    rc = _lib.lib().rh_gemv_int8(W.data_ptr(), ldw, S.data_ptr(), int(f16_scale), X.data_ptr(), Y.data_ptr(), T, K,
+                                 N, beta, None)
     _lib.check(rc, "rh_gemv_int8")
     torch.cuda.synchronize()
     return Y.cpu().numpy()
@@ -78,16 +82,31 @@ def test_fp16_scales(torch_mod, dev):
 
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
 def test_llama3_shapes(torch_mod, dev, N, K):
-    """BASELINE config 4's projection shapes at T = 8 (fp16 scales)."""
+    """BASELINE config 4's projection shapes at T = 8 (fp16 scales), in the padded row
+    layout the backend stores (rh_gemv_int8_row_stride)."""
+    from relay_amd import _lib
+
     w8, s, x = make(N, K, 8, seed=N + K)
     s16 = bits_to_f32(f16_bits(s))
-    y = run(torch_mod, dev, w8, s, x, f16_scale=True)
+    ldw = _lib.lib().rh_gemv_int8_row_stride(K)
+    y = run(torch_mod, dev, w8, s, x, f16_scale=True, ldw=ldw)
     exact = O.gemv_int8(w8, s16, x)
     assert (np.abs(y - exact) <= bound(w8, s16, x)).all()
+
+
+@pytest.mark.parametrize("ldw", [96, 160, 4096 + 256])
+def test_row_stride_gives_the_same_bits(torch_mod, dev, ldw):
+    """Rows ldw bytes apart (junk in the padding): bit-identical to the dense layout."""
+    w8, s, x = make(300, 96, 4, seed=ldw)
+    a = run(torch_mod, dev, w8, s, x)
+    b = run(torch_mod, dev, w8, s, x, ldw=ldw)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_rejects_bad_shapes(torch_mod, dev):
     from relay_amd import _lib
 
-    assert _lib.lib().rh_gemv_int8(None, None, 0, None, None, 17, 64, 64, 0.0, None) != 0
-    assert _lib.lib().rh_gemv_int8(None, None, 0, None, None, 1, 72, 64, 0.0, None) != 0
+    assert _lib.lib().rh_gemv_int8(None, 64, None, 0, None, None, 17, 64, 64, 0.0, None) != 0
+    assert _lib.lib().rh_gemv_int8(None, 72, None, 0, None, None, 1, 72, 64, 0.0, None) != 0
+    assert _lib.lib().rh_gemv_int8(None, 48, None, 0, None, None, 1, 64, 64, 0.0, None) != 0
+    assert "ldw" in _lib.last_error()

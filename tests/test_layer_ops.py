@@ -55,12 +55,20 @@ def test_quantize_int8_bit_exact(torch_mod, dev):
     w[5, :7] = [0.5, -0.5, 0.25, 1.0, -1.0, 127.0 / 254.0, 3.0 / 254.0]  # halfway cases for rint
     q_want, s_want = O.quantize_int8(w)
     W = torch_mod.from_numpy(w).to(dev)
-    Q = torch_mod.empty(w.shape, dtype=torch_mod.int8, device=dev)
+    ldq = 1024 + 256  # padded rows: the bytes past K stay as they were
+    Q = torch_mod.full((w.shape[0], ldq), 55, dtype=torch_mod.int8, device=dev)
     S = torch_mod.empty(w.shape[0], dtype=torch_mod.float32, device=dev)
-    _lib.check(_lib.lib().rh_quantize_int8(W.data_ptr(), w.shape[0], w.shape[1], Q.data_ptr(), S.data_ptr(), None))
+    _lib.check(_lib.lib().rh_quantize_int8(W.data_ptr(), w.shape[0], w.shape[1], Q.data_ptr(), ldq, S.data_ptr(), None))
     torch_mod.cuda.synchronize()
     assert np.array_equal(S.cpu().numpy().view(np.uint32), s_want.view(np.uint32))
-    assert np.array_equal(Q.cpu().numpy(), q_want)
+    q = Q.cpu().numpy()
+    assert np.array_equal(q[:, :w.shape[1]], q_want) and (q[:, w.shape[1]:] == 55).all()
+    # dequant from the padded rows: fp16(q * scale), dense output
+    D = torch_mod.empty(w.shape, dtype=torch_mod.float16, device=dev)
+    _lib.check(_lib.lib().rh_dequant_int8(Q.data_ptr(), ldq, S.data_ptr(), w.shape[0], w.shape[1], D.data_ptr(), None))
+    torch_mod.cuda.synchronize()
+    want = (q_want.astype(np.float32) * s_want[:, None]).astype(np.float16)
+    assert np.array_equal(D.cpu().numpy().view(np.uint16), want.view(np.uint16))
 
 
 def test_kv_gather_scatter_round_trip(torch_mod, dev):

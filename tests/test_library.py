@@ -55,7 +55,9 @@ def test_no_device_means_an_error_not_a_fallback():
 
 def test_kernel_launchers_validate_shapes_before_launching():
     lib = _lib.lib()
-    assert lib.rh_gemv_int8(None, None, 0, None, None, 0, 64, 64, 0.0, None) != 0
+    assert lib.rh_gemv_int8(None, 64, None, 0, None, None, 0, 64, 64, 0.0, None) != 0
+    assert lib.rh_gemv_int8_row_stride(4096) == 4096 + 256 and lib.rh_gemv_int8_row_stride(576) == 576
+    assert lib.rh_gemv_int8_row_stride(14336) == 14336 + 256 and lib.rh_gemv_int8_row_stride(100) == 112
     assert "T must be" in _lib.last_error()
     assert lib.rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64, None) != 0
     assert lib.rh_prefill_tile_rows() == 128
