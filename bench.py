@@ -337,6 +337,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3"],
+                    help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters under rocprofv3 --pmc)")
@@ -360,6 +362,20 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": 256 << 20, "launches": 20}))
+        return
+
+    if args.leg:
+        if args.leg == "prefill":
+            r = bench_prefill(torch, dev, stream, args.steps, args.warmup)
+        elif args.leg == "prefill128":
+            r = bench_prefill(torch, dev, stream, args.steps, args.warmup, heads=32, kvh=8, D=128)
+        elif args.leg == "gemv":
+            r = bench_gemv(torch, dev, stream, args.steps, args.warmup)
+        elif args.leg == "config1":
+            r = bench_config1()
+        else:
+            r = bench_llama3_mixed(args.steps)
+        print(json.dumps({"leg": args.leg, **r}), flush=True)
         return
 
     dec = bench_decode(torch, dev, stream, args.steps, args.warmup)
