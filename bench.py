@@ -382,7 +382,7 @@ def main():
     log(f"decode attention: {dec['ms'] * 1e3:.2f} us/launch, {dec['gbs']:.0f} GB/s")
     extra = {}
     if not args.quick:
-        pre = bench_prefill(torch, dev, stream, max(10, args.steps // 10), 3)
+        pre = bench_prefill(torch, dev, stream, 50, 20)  # enough warmup for the clocks to settle
         log(f"prefill attention: {pre['ms'] * 1e3:.1f} us, {pre['tflops']:.1f} TFLOP/s")
         extra["prefill_attention"] = {"workload": "2048-token causal prefill, 32q/4kv heads, D64 (config 3)",
                                       "us": round(pre["ms"] * 1e3, 2), "tflops": round(pre["tflops"], 1),

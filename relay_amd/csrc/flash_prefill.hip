@@ -9,20 +9,20 @@
 //   block of up to 128 consecutive rows of one chunk, or a pair of blocks (i, n-1-i) of
 //   the same chunk processed one after the other, so that every workgroup does the same
 //   causal work (rh_prefill_plan makes the items; it pairs when the grid is large).
-// - Waves 2r and 2r+1 own the block's rows 32r .. 32r+31 and split every 64-key tile:
-//   keys 0-31 go to the even wave, 32-63 to the odd one. Each keeps its own running max,
-//   sum and O^T; at the end of the block the odd wave hands them to the even one through
-//   LDS. So two waves stay busy on every SIMD until the block's last tile (with one wave
+// - Waves 2r and 2r+1 own the block's rows 32r .. 32r+31 and split every key tile (128
+//   keys at head_dim 64, 64 at 128): the first half goes to the even wave, the second to
+//   the odd one. Each keeps its own running max, sum and O^T; at the end of the block the
+//   odd wave hands them to the even one through LDS. So two waves stay busy on every SIMD until the block's last tile (with one wave
 //   per 32-row strip, every SIMD drops to one wave once the short blocks finish).
-// - The workgroup walks the keys 0 .. (block's last position) 64 at a time: each tile of K
-//   and V is gathered through the block table into registers one tile ahead (its block
+// - The workgroup walks the keys 0 .. (block's last position) a tile at a time: each tile
+//   of K and V is gathered through the block table into registers one tile ahead (its block
 //   ids another tile ahead) and written to one of two LDS buffers (one barrier per tile).
-// - Per wave and 32-key half tile:
+// - Per wave and half tile (one or two 32-key sub-steps, whose S^T chains interleave):
 //     S^T[32 keys x 32 rows] = K[32 keys x D] * Q^T[D x 32 rows]        (D/16 MFMA 32x32x16)
 //     online softmax per row (lane = row): reductions over the lane's 16 registers plus
 //     one swap with lane l^32; scale and log2(e) folded into one FMA per score; the row
 //     sum from the fp16 P values with packed dot products
-//     O^T[D x 32 rows] += V^T[D x 32 keys] * P^T[32 keys x 32 rows]      (D/16 MFMA 32x32x16)
+//     O^T[D x 32 rows] += V^T[D x 16 keys] * P^T[16 keys x 32 rows]     (D/32 MFMA 32x32x16)
 //   The S^T accumulators are the P^T B operands as they stand. Lane (c, h) of S^T holds
 //   keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key group, so V is stored transposed with
 //   the keys of each 16-key group permuted to that order: the V^T A operand of an MFMA is
@@ -46,7 +46,11 @@ namespace {
 constexpr int kRows = 128;    // query rows per block
 constexpr int kWaves = 8;     // two per 32-row strip
 constexpr int kThreads = kWaves * kWave;
-constexpr int kKeyTile = 64;  // keys per LDS tile
+// 32-key sub-steps per wave per tile: at D 64 two independent S^T chains per wave under
+// one softmax (measured 45.0 -> 41.8 us at config 3); at D 128 the second chain's
+// registers would spill.
+template <int D>
+constexpr int sub_steps() { return D == 64 ? 2 : 1; }
 
 // One work item: block a (t0, rows, first position), block b likewise (rows 0: none), and
 // the chunk's block-table offset. Layout of rh_prefill_plan's int32[8] records.
@@ -77,6 +81,8 @@ __device__ __forceinline__ int vperm(int k) {
 
 template <int D, bool POW2>
 __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillArgs a) {
+  constexpr int kSub = sub_steps<D>();      // 32-key sub-steps per wave per tile
+  constexpr int kKeyTile = 64 * kSub;       // keys per LDS tile
   constexpr int CH = D / 8;                                 // 16-byte chunks per row
   constexpr int MK = D / 16;                                // QK MFMAs per half tile
   constexpr int DT = D / 32;                                // 32-dim tiles of O^T
@@ -199,39 +205,48 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
       for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
     float m_run = -INFINITY, l_part = 0.0f;
 
-    // This wave's 32 keys of the tile in LDS buffer `buf` starting at key k0.
+    // This wave's 32 kSub keys of the tile in LDS buffer `buf` starting at key k0.
     auto compute = [&](int buf, int k0) {
-      const int kb = k0 + 32 * half;
+      const int kb = k0 + 32 * kSub * half;
       if (!wave_on || kb > wave_last) return;  // uniform per wave
-      float16v s;
+      float16v s[kSub];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-      const half_t* kt = sK + buf * KBUF + (32 * half + c) * D;
+      for (int j = 0; j < kSub; ++j)
 #pragma unroll
-      for (int m = 0; m < MK; ++m) {
-        const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz(c)) << 3));
-        s = mfma32x32x16(ka, qb[m], s);
-      }
-      // Causal mask only where the half tile crosses a row of this strip.
-      const bool need_mask = kb + 31 > p0 + strip * 32;
+        for (int r = 0; r < 16; ++r) s[j][r] = 0.0f;
+#pragma unroll
+      for (int m = 0; m < MK; ++m)
+#pragma unroll
+        for (int j = 0; j < kSub; ++j) {
+          const half_t* kt = sK + buf * KBUF + (32 * kSub * half + 32 * j + c) * D;
+          const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz(c)) << 3));
+          s[j] = mfma32x32x16(ka, qb[m], s[j]);
+        }
+      // Causal mask only where the keys cross a row of this strip.
+      const bool need_mask = kb + 32 * kSub - 1 > p0 + strip * 32;
       float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (need_mask && key > qpos) s[r] = -INFINITY;
-        mx = fmaxf(mx, s[r]);
-      }
+      for (int j = 0; j < kSub; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * j + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (need_mask && key > qpos) s[j][r] = -INFINITY;
+          mx = fmaxf(mx, s[j][r]);
+        }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float base = m_new == -INFINITY ? 0.0f : m_new * cl;
       const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(__builtin_fmaf(m_run, cl, -base));
-      half8 pb[2];
+      half8 pb[2 * kSub];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pb[r >> 3][r & 7] = static_cast<half_t>(fast_exp2(__builtin_fmaf(s[r], cl, -base)));
+      for (int j = 0; j < kSub; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          pb[2 * j + (r >> 3)][r & 7] = static_cast<half_t>(fast_exp2(__builtin_fmaf(s[j][r], cl, -base)));
       // Row sum of the fp16 P values (the ones the PV product uses), fp32 accumulation.
       float psum = 0.0f;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < 2 * kSub; ++u)
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           const half2_t p2 = {pb[u][e], pb[u][e + 1]};
@@ -247,12 +262,12 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
       }
       m_run = m_new;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < 2 * kSub; ++u)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int d = 32 * dt + c;
           const half8 va = *reinterpret_cast<const half8*>(sVt + buf * VBUF + d * kKeyTile +
-                                                           (((4 * half + 2 * u + hh) ^ vswz(d)) << 3));
+                                                           (((4 * kSub * half + 2 * u + hh) ^ vswz(d)) << 3));
           o[dt] = mfma32x32x16(va, pb[u], o[dt]);
         }
     };
