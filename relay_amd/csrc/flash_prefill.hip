@@ -35,6 +35,7 @@
 //   the K/V its workgroups re-read.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/relay_hip.h"
@@ -206,9 +207,11 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
     float m_run = -INFINITY, l_part = 0.0f;
 
     // This wave's 32 kSub keys of the tile in LDS buffer `buf` starting at key k0.
-    auto compute = [&](int buf, int k0) {
-      const int kb = k0 + 32 * kSub * half;
-      if (!wave_on || kb > wave_last) return;  // uniform per wave
+    // MASK: the keys cross a row of this strip (only the diagonal tiles); a separate
+    // instantiation, because a uniform branch around the selects is if-converted into
+    // per-element work on every tile.
+    auto compute = [&](auto mask_tag, int buf, int kb) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       float16v s[kSub];
 #pragma unroll
       for (int j = 0; j < kSub; ++j)
@@ -222,15 +225,13 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
           const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz(c)) << 3));
           s[j] = mfma32x32x16(ka, qb[m], s[j]);
         }
-      // Causal mask only where the keys cross a row of this strip.
-      const bool need_mask = kb + 32 * kSub - 1 > p0 + strip * 32;
       float mx = -INFINITY;
+      const int lim = qpos - kb - 4 * hh;  // key offsets above this are masked
 #pragma unroll
       for (int j = 0; j < kSub; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * j + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (need_mask && key > qpos) s[j][r] = -INFINITY;
+          if (MASK && 32 * j + 8 * (r >> 2) + (r & 3) > lim) s[j][r] = -INFINITY;
           mx = fmaxf(mx, s[j][r]);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -283,12 +284,25 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
     __syncthreads();
     if (ntiles > 1) fetch(kKeyTile);
     if (ntiles > 2) lookup(2 * kKeyTile);
-    for (int j = 0; j < ntiles; ++j) {
-      compute(j & 1, j * kKeyTile);
+    // Tiles before j_mask lie wholly at or below this strip's first row: no mask code runs
+    // for them. Every wave runs ntiles steps (the barriers match); only the split differs.
+    const int first_masked = p0 + strip * 32 - 32 * kSub * (half + 1) + 1;  // unmasked: j * kKeyTile <= this
+    const int j_mask = min(ntiles, first_masked >= 0 ? first_masked / kKeyTile + 1 : 0);
+    auto advance = [&](int j) {
       if (j + 1 < ntiles) store((j + 1) & 1);
       __syncthreads();
       if (j + 2 < ntiles) fetch((j + 2) * kKeyTile);
       if (j + 3 < ntiles) lookup((j + 3) * kKeyTile);
+    };
+    int j = 0;
+    for (; j < j_mask; ++j) {
+      if (wave_on) compute(std::false_type{}, j & 1, j * kKeyTile + 32 * kSub * half);
+      advance(j);
+    }
+    for (; j < ntiles; ++j) {
+      const int kb = j * kKeyTile + 32 * kSub * half;
+      if (wave_on && kb <= wave_last) compute(std::true_type{}, j & 1, kb);  // uniform per wave
+      advance(j);
     }
 
     // Merge the strip's two halves: the odd wave's (max, sum, O^T) through LDS (the tile
