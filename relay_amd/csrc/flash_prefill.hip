@@ -235,7 +235,10 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
           mx = fmaxf(mx, s[j][r]);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
+      // Lazy rescaling: a row keeps its reference maximum until a score exceeds it by more
+      // than 2^8 in the exp2 domain (P <= 256 stays exact to fp16's 11 bits, sums fit in
+      // fp32), so O^T is rescaled on a handful of tiles instead of most of them.
+      const float m_new = (mx - m_run) * cl > 8.0f ? mx : m_run;  // m_run = -inf: takes mx
       const float base = m_new == -INFINITY ? 0.0f : m_new * cl;
       const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(__builtin_fmaf(m_run, cl, -base));
       half8 pb[2 * kSub];
