@@ -276,36 +276,36 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
         }
     };
 
-    // Tile j lives in LDS buffer j & 1; while it is computed, tile j+1's rows are in flight
-    // into registers and tile j+2's block ids are being read.
+    // Tile j lives in LDS buffer j & 1. Step j: store tile j+1 (rows fetched a step ago)
+    // into the other buffer, issue tile j+2's loads and tile j+3's block ids, compute
+    // tile j, barrier; the loads are in flight under the compute.
     const int ntiles = (nkeys + kKeyTile - 1) / kKeyTile;
     __syncthreads();  // the previous phase's merge is done with the LDS
     lookup(0);
     fetch(0);
     if (ntiles > 1) lookup(kKeyTile);
     store(0);
-    __syncthreads();
     if (ntiles > 1) fetch(kKeyTile);
     if (ntiles > 2) lookup(2 * kKeyTile);
-    // Tiles before j_mask lie wholly at or below this strip's first row: no mask code runs
-    // for them. Every wave runs ntiles steps (the barriers match); only the split differs.
+    __syncthreads();
     const int first_masked = p0 + strip * 32 - 32 * kSub * (half + 1) + 1;  // unmasked: j * kKeyTile <= this
     const int j_mask = min(ntiles, first_masked >= 0 ? first_masked / kKeyTile + 1 : 0);
-    auto advance = [&](int j) {
+    auto prepare = [&](int j) {
       if (j + 1 < ntiles) store((j + 1) & 1);
-      __syncthreads();
       if (j + 2 < ntiles) fetch((j + 2) * kKeyTile);
       if (j + 3 < ntiles) lookup((j + 3) * kKeyTile);
     };
     int j = 0;
     for (; j < j_mask; ++j) {
+      prepare(j);
       if (wave_on) compute(std::false_type{}, j & 1, j * kKeyTile + 32 * kSub * half);
-      advance(j);
+      __syncthreads();
     }
     for (; j < ntiles; ++j) {
+      prepare(j);
       const int kb = j * kKeyTile + 32 * kSub * half;
       if (wave_on && kb <= wave_last) compute(std::true_type{}, j & 1, kb);  // uniform per wave
-      advance(j);
+      __syncthreads();
     }
 
     // Merge the strip's two halves: the odd wave's (max, sum, O^T) through LDS (the tile
