@@ -337,7 +337,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3"],
+    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3", "tinyllama"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
@@ -373,6 +373,8 @@ def main():
             r = bench_gemv(torch, dev, stream, args.steps, args.warmup)
         elif args.leg == "config1":
             r = bench_config1()
+        elif args.leg == "tinyllama":
+            r = bench_tinyllama_decode(args.steps)
         else:
             r = bench_llama3_mixed(args.steps)
         print(json.dumps({"leg": args.leg, **r}), flush=True)

@@ -141,6 +141,17 @@ int64_t rh_gemv_int8_row_stride(int K);
 /* Largest T rh_gemv_int8 takes. */
 int rh_gemv_int8_max_tokens(void);
 
+/* y[t, n] = sum_k W16[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for 1 <= T <= 32:
+ * the dense projection at decode batch sizes. W16 fp16 [N, K] rows ldw elements apart
+ * (ldw >= K, a multiple of 8); x fp16 [T, K]; y fp32 [T, N]; K a multiple of 16; W16 and x
+ * 16-byte aligned. fp32 accumulation of exact fp16 products in a fixed order.
+ * Replaces cublasGemmEx (cuda_backend.cu:726-730) where T is small. */
+int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
+                void* stream);
+
+/* Largest T rh_gemv_f16 takes. */
+int rh_gemv_f16_max_tokens(void);
+
 /* Per-row symmetric int8 quantization of an fp32 matrix [N, K] on the device:
  * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale),
  * q rows ldq bytes apart (ldq >= K; the bytes past K are not written).

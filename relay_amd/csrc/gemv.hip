@@ -1,6 +1,8 @@
-// Weight-only int8 GEMV for decode batches (T <= 16 tokens) on gfx950.
+// Skinny products for decode batches on gfx950: weight-only int8 (T <= 16 tokens) and fp16
+// weights (T <= 32 tokens).
 //
-//   y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n])
+//   y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n])       rh_gemv_int8
+//   y[t, n] =            sum_k W16[n, k] * x[t, k] (+ beta * y[t, n])       rh_gemv_f16
 //
 // relay's gemv_int8_kernel (cuda_kernels.cuh:364-430) does the products on the vector
 // ALU, once per token. Here the products run on the matrix cores instead: a 16-row tile
@@ -23,6 +25,12 @@
 // matching 32 bytes of token c's activation row (zero for c >= T). Eight (or sixteen)
 // waves per workgroup split K; their 16x16 accumulators are summed in LDS in a fixed
 // order, so results do not depend on timing.
+//
+// The fp16 kernel has the same shape: lane (c, g) loads the 32 bytes W16[n0 + c, k0 + 16g
+// .. +16) of a 64-k chunk as the A operands of two MFMAs, and up to 32 tokens are two
+// 16-column B blocks sharing them. It replaces the dense GEMM library call at decode batch
+// sizes, where that call spends ~8 us on matrices whose weights stream in well under 1 us
+// (relay uses cublasGemmEx at every T, cuda_backend.cu:726-730).
 #include "../../include/relay_hip.h"
 #include "common.h"
 
@@ -114,6 +122,79 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   }
 }
 
+// fp16 weights, T <= 16 * NB tokens (NB column blocks of 16 tokens share each A operand).
+template <int WAVES, int NB>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* __restrict__ wt, int64_t ldw,
+                                                                 const half_t* __restrict__ x, float* y, int T,
+                                                                 int K, int N, float beta) {
+  __shared__ float red[WAVES][NB][kWave * 4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int row = min(n0 + c, N - 1);
+  const int nchunks = (K + kChunk - 1) / kChunk;
+  const int per = (nchunks + WAVES - 1) / WAVES;
+  const int cb = w * per, ce = min(nchunks, cb + per);
+  const half_t* wrow = wt + static_cast<int64_t>(row) * ldw;
+  bool tok[NB];
+  const half_t* xrow[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    tok[b] = 16 * b + c < T;
+    xrow[b] = x + static_cast<int64_t>(tok[b] ? 16 * b + c : 0) * K;
+  }
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  float4v acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = cb; q0 < ce; q0 += kUnroll) {
+    half8 wa[kUnroll], wb[kUnroll], xa[NB][kUnroll], xb[NB][kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int k = (q0 + u) * kChunk + 16 * g;
+      const bool live = q0 + u < ce && k < K;
+      wa[u] = live ? load_half8(wrow + k) : zero;
+      wb[u] = live ? load_half8(wrow + k + 8) : zero;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
+        xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        acc[b] = mfma16x16x32(wa[u], xa[b][u], acc[b]);
+        acc[b] = mfma16x16x32(wb[u], xb[b][u], acc[b]);
+      }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][b][lane * 4 + r] = acc[b][r];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    // Lane (c, g) sums the waves for token 16b + c, rows n0 + 4g + r, in a fixed order.
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] += red[ww][b][lane * 4 + r];
+    if (!tok[b]) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = n0 + 4 * g + r;
+      if (n >= N) continue;
+      float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+      *dst = s[r] + (beta != 0.0f ? beta * *dst : 0.0f);
+    }
+  }
+}
+
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
@@ -152,4 +233,36 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
   const half_t* xh = static_cast<const half_t*>(x);
   return scale_is_f16 ? launch<true>(w8, ldw, scale, xh, y, T, K, N, beta, s)
                       : launch<false>(w8, ldw, scale, xh, y, T, K, N, beta, s);
+}
+
+extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
+
+extern "C" int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
+                           void* stream) {
+  RH_REQUIRE(T >= 1 && T <= 2 * kMaxTokens, "gemv_f16: T must be in 1..32");
+  RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_f16: K must be a positive multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemv_f16: W16 and x must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const half_t* wt = static_cast<const half_t*>(w16);
+  const half_t* xh = static_cast<const half_t*>(x);
+  const int tiles = (N + 15) / 16;
+  const bool wide = tiles < 256;
+  if (T <= kMaxTokens) {
+    if (wide) {
+      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<16, 1>), dim3(tiles), dim3(16 * kWave), 0, s, wt, ldw, xh, y,
+                                       T, K, N, beta));
+    } else {
+      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<8, 1>), dim3(tiles), dim3(8 * kWave), 0, s, wt, ldw, xh, y,
+                                       T, K, N, beta));
+    }
+  } else if (wide) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<16, 2>), dim3(tiles), dim3(16 * kWave), 0, s, wt, ldw, xh, y,
+                                     T, K, N, beta));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<8, 2>), dim3(tiles), dim3(8 * kWave), 0, s, wt, ldw, xh, y, T,
+                                     K, N, beta));
+  }
+  return 0;
 }

@@ -328,6 +328,12 @@ void HipBackend::load_weights(const WeightSource& src) {
 }
 
 void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta) {
+  // Decode batch sizes: the skinny MFMA kernel (the library GEMM spends ~8 us per call on
+  // small matrices). Measured crossover: the library is as fast from T = 16 to 24 up.
+  if (T <= 16 && K % 16 == 0) {
+    RH_CHECK(rh_gemv_f16(W, K, x, y, T, K, N, beta, stream_));
+    return;
+  }
   // Row-major y[T, N] = x[T, K] W[N, K]^T is column-major y^T (N x T) = W^T-view (K x N)^T x^T.
   const float alpha = 1.0f;
   ROCBLAS_CHECK(rocblas_gemm_ex(blas_, rocblas_operation_transpose, rocblas_operation_none, N, T, K, &alpha, W,

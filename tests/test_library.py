@@ -29,7 +29,7 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    for want in ("rh_paged_decode_attention", "rh_flash_prefill", "rh_gemv_int8", "relay_hip_backend_forward",
+    for want in ("rh_paged_decode_attention", "rh_flash_prefill", "rh_gemv_int8", "rh_gemv_f16", "relay_hip_backend_forward",
                  "relay_hip_backend_read_kv_layer", "relay_hip_backend_update_weight"):
         assert want in names
 
