@@ -373,11 +373,13 @@ extern "C" int rh_decode_chunk_keys(int head_dim) {
 extern "C" int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int max_ctx) {
   const int chunk = rh_decode_chunk_keys(head_dim);
   if (chunk <= 0 || n_dec <= 0 || max_ctx <= 0) return chunk;
-  // Measured on MI355X (32 x 2048 / D64 up to 48 x 8192 / D128): at least two slices per
+  // Measured on MI355X (1 x 640 / D64 up to 48 x 8192 / D128): one slice for at most 16
+  // (context, kv head) groups of at most 16 chunks; otherwise at least two slices per
   // context (enough workgroups to spread over the 256 CUs), more while there are fewer
-  // than 256 (context, kv head) groups, but never below 8 chunks (one per wave of an
-  // 8-wave workgroup).
+  // than 256 groups, but never below 8 chunks (one per wave of an 8-wave workgroup).
   const long groups = static_cast<long>(n_dec) * kv_heads * ((group + 15) / 16);
+  // A handful of short contexts: one slice (no merge); the launch is latency-bound anyway.
+  if (groups <= 16 && max_ctx <= 16 * chunk) return (max_ctx + chunk - 1) / chunk * chunk;
   const long parts = std::max(2L, 256 / groups);
   const long per_part = (max_ctx + parts - 1) / parts;
   const long keys = std::max(8L * chunk, (per_part + chunk - 1) / chunk * chunk);
