@@ -230,11 +230,17 @@ def bench_config1(prompt_len=512, new_tokens=128):
     be = HipBackend(None, nb, bs, max_batch_tokens=2048, options=HipOptions(False, False), config=c,
                     synthetic_seed=0, synthetic_std=0.02)
     prompt = np.random.default_rng(0).integers(0, c.vocab, size=prompt_len).tolist()
-    marks = []
+    marks, dev_ms = [], []
     runs = []
     for rep in range(3):  # the first run warms up
         marks.clear()
-        eng = GreedyEngine(be, nb, bs, 2048, 8, on_logits=lambda rid, i, row: marks.append(time.perf_counter()))
+        dev_ms.clear()
+
+        def seen(rid, i, row):
+            marks.append(time.perf_counter())
+            dev_ms.append(be.last_forward_ms())
+
+        eng = GreedyEngine(be, nb, bs, 2048, 8, on_logits=seen)
         eng.add(1, prompt, new_tokens)
         t0 = time.perf_counter()
         out = eng.run_all()[1]
@@ -244,6 +250,7 @@ def bench_config1(prompt_len=512, new_tokens=128):
     be.close()
     prefill, decode, total = (float(np.median([r[i] for r in runs[1:]])) for i in range(3))
     return {"prompt_ms": round(prefill * 1e3, 2), "decode_tok_s": round((new_tokens - 1) / decode, 1),
+            "decode_step_ms_device": round(float(np.median(dev_ms[1:])), 3),
             "total_s": round(total, 4), "gen_tok_s": round(new_tokens / total, 1)}
 
 

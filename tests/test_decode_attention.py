@@ -145,6 +145,14 @@ def test_config2_full_size(torch_mod, dev):
         check_close(g, want)
 
 
+def test_config5_full_size(torch_mod, dev):
+    """BASELINE config 5's decode part at full size: 48 sequences x 8192 context, 32 q / 8 kv
+    heads, D 128, bs 16 (1.6 GB of K+V for the layer)."""
+    case = PagedCase([8192] * 48, 1, 32, 8, 128, 16, seed=5, extra_blocks=0)
+    g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
 def test_rejects_unsupported_shapes(torch_mod, dev):
     from relay_amd import _lib
 
