@@ -149,6 +149,19 @@ int rh_gemv_int8_max_tokens(void);
 int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
                 void* stream);
 
+/* rh_gemv_f16 with the producer of x folded in (no counterpart in relay, where
+ * rms_norm_kernel / silu_mul_kernel run as their own launches before the GEMM,
+ * cuda_backend.cu:576-591). Each workgroup computes x for all T tokens into LDS:
+ *   _rmsnorm: x fp32 [T, K] -> fp16(norm_w[k] * (x * 1/sqrt(mean_k(x^2) + eps))), the row's
+ *             sum of squares in double (rh_rmsnorm's arithmetic);
+ *   _silu:    gu fp32 [T, 2K] (gate | up) -> fp16(g / (1 + exp(-g)) * u) (rh_silu_mul's).
+ * Requires rh_gemv_f16_fused_fits(T, K) (T * (K + 8) fp16 values fit 64 KB of LDS). */
+int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps, float* y,
+                        int T, int K, int N, float beta, void* stream);
+int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N, float beta,
+                     void* stream);
+int rh_gemv_f16_fused_fits(int T, int K);
+
 /* Largest T rh_gemv_f16 takes. */
 int rh_gemv_f16_max_tokens(void);
 

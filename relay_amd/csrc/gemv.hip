@@ -38,6 +38,7 @@ namespace relay_hip {
 namespace {
 
 constexpr int kMaxTokens = 16;
+constexpr size_t kFusedLdsBytes = 64 << 10;  // staged activations of the fused fp16 products
 constexpr int kChunk = 64;   // k per wave step
 constexpr int kUnroll = 4;   // chunks whose loads are issued together
 
@@ -122,12 +123,25 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   }
 }
 
+// What the fp16 kernel's B operands are made from:
+//   kPlain   x fp16 [T, K], loaded per lane;
+//   kRmsNorm x fp32 [T, K] (the residual stream): fp16(w[k] * (x * 1/sqrt(mean(x^2) + eps)))
+//            with the row's sum of squares in double (rmsnorm_kernel's arithmetic);
+//   kSiluMul x fp32 [T, 2K] (gate | up): fp16(g / (1 + exp(-g)) * u) (silu_mul_kernel's);
+// the last two are computed once per workgroup into LDS (rows K + 8 halves apart), which
+// saves the separate normalisation / activation launch at decode batch sizes.
+enum Prologue { kPlain = 0, kRmsNorm = 1, kSiluMul = 2 };
+
 // fp16 weights, T <= 16 * NB tokens (NB column blocks of 16 tokens share each A operand).
-template <int WAVES, int NB>
+template <int WAVES, int NB, int PRO>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* __restrict__ wt, int64_t ldw,
-                                                                 const half_t* __restrict__ x, float* y, int T,
-                                                                 int K, int N, float beta) {
+                                                                 const void* __restrict__ xin,
+                                                                 const float* __restrict__ norm_w, float eps,
+                                                                 float* y, int T, int K, int N, float beta) {
   __shared__ float red[WAVES][NB][kWave * 4];
+  __shared__ float s_inv[2 * kMaxTokens];
+  extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
+  const half_t* x = static_cast<const half_t*>(xin);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
@@ -144,6 +158,32 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     xrow[b] = x + static_cast<int64_t>(tok[b] ? 16 * b + c : 0) * K;
   }
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int XR = K + 8;
+  if (PRO == kRmsNorm) {
+    const float* xf = static_cast<const float*>(xin);
+    for (int t = w; t < T; t += WAVES) {
+      double ss = 0;
+      for (int i = lane; i < K; i += kWave) ss += static_cast<double>(xf[static_cast<int64_t>(t) * K + i]) *
+                                                 xf[static_cast<int64_t>(t) * K + i];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      if (lane == 0) s_inv[t] = 1.0f / sqrtf(static_cast<float>(ss / K) + eps);
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
+      const int t = idx / K, i = idx - t * K;
+      sxb[t * XR + i] = static_cast<half_t>(norm_w[i] * (xf[static_cast<int64_t>(t) * K + i] * s_inv[t]));
+    }
+    __syncthreads();
+  } else if (PRO == kSiluMul) {
+    const float* gu = static_cast<const float*>(xin);
+    for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
+      const int t = idx / K, i = idx - t * K;
+      const float v = gu[static_cast<int64_t>(t) * 2 * K + i];
+      sxb[t * XR + i] = static_cast<half_t>(v / (1.0f + expf(-v)) * gu[static_cast<int64_t>(t) * 2 * K + K + i]);
+    }
+    __syncthreads();
+  }
 
   float4v acc[NB];
 #pragma unroll
@@ -158,8 +198,15 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
       wb[u] = live ? load_half8(wrow + k + 8) : zero;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
-        xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
+        if (PRO == kPlain) {
+          xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
+          xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
+        } else {
+          // Columns past T read a real row (never written out); chunks past K read nothing.
+          const half_t* xs = sxb + min(16 * b + c, T - 1) * XR + k;
+          xa[b][u] = live ? *reinterpret_cast<const half8*>(xs) : zero;
+          xb[b][u] = live ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+        }
       }
     }
 #pragma unroll
@@ -237,32 +284,55 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
 
 extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
 
-extern "C" int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
-                           void* stream) {
+template <int PRO>
+static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const float* norm_w, float eps, float* y,
+                           int T, int K, int N, float beta, void* stream) {
   RH_REQUIRE(T >= 1 && T <= 2 * kMaxTokens, "gemv_f16: T must be in 1..32");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_f16: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_f16: W16 and x must be 16-byte aligned");
+  const size_t lds = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
+  RH_REQUIRE(lds <= kFusedLdsBytes, "gemv_f16: T * (K + 8) fp16 activations exceed the fused path's LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* wt = static_cast<const half_t*>(w16);
-  const half_t* xh = static_cast<const half_t*>(x);
   const int tiles = (N + 15) / 16;
   const bool wide = tiles < 256;
+#define RH_GEMV_F16(W, NBLK)                                                                                    \
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO>), dim3(tiles), dim3(W * kWave), lds, s, wt, ldw, \
+                                   x, norm_w, eps, y, T, K, N, beta))
   if (T <= kMaxTokens) {
     if (wide) {
-      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<16, 1>), dim3(tiles), dim3(16 * kWave), 0, s, wt, ldw, xh, y,
-                                       T, K, N, beta));
+      RH_GEMV_F16(16, 1);
     } else {
-      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<8, 1>), dim3(tiles), dim3(8 * kWave), 0, s, wt, ldw, xh, y,
-                                       T, K, N, beta));
+      RH_GEMV_F16(8, 1);
     }
   } else if (wide) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<16, 2>), dim3(tiles), dim3(16 * kWave), 0, s, wt, ldw, xh, y,
-                                     T, K, N, beta));
+    RH_GEMV_F16(16, 2);
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<8, 2>), dim3(tiles), dim3(8 * kWave), 0, s, wt, ldw, xh, y, T,
-                                     K, N, beta));
+    RH_GEMV_F16(8, 2);
   }
+#undef RH_GEMV_F16
   return 0;
+}
+
+extern "C" int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
+                           void* stream) {
+  return gemv_f16_launch<kPlain>(w16, ldw, x, nullptr, 0.0f, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
+                                   float* y, int T, int K, int N, float beta, void* stream) {
+  RH_REQUIRE(norm_w != nullptr, "gemv_f16_rmsnorm: no norm weights");
+  return gemv_f16_launch<kRmsNorm>(w16, ldw, x, norm_w, eps, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N,
+                                float beta, void* stream) {
+  return gemv_f16_launch<kSiluMul>(w16, ldw, gu, nullptr, 0.0f, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_f16_fused_fits(int T, int K) {
+  return T >= 1 && T <= 2 * kMaxTokens && K > 0 &&
+         static_cast<size_t>(T) * (K + 8) * sizeof(half_t) <= kFusedLdsBytes;
 }

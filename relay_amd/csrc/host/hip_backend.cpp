@@ -179,6 +179,7 @@ class HipBackend final : public Backend {
   DeviceArray<float> make_f32(const float* host, std::size_t n, float fill);
   void upload_f32_rows(const float* host, int N, int K, const std::function<void(const float*, int, int)>& apply);
   void gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta);
+  bool fused(const DeviceMatrix& W, int T) const;
   void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
   void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
 
@@ -342,6 +343,11 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
                                 rocblas_gemm_algo_standard, 0, 0));
 }
 
+bool HipBackend::fused(const DeviceMatrix& W, int T) const {
+  // Normalisation / activation folded into the skinny fp16 product (same T range as gemm_f16's).
+  return !W.i8.p && T <= 16 && W.K % 16 == 0 && rh_gemv_f16_fused_fits(T, W.K);
+}
+
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
   if (T <= rh_gemv_int8_max_tokens()) {
@@ -459,8 +465,12 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     DeviceLayer& L = layers_[l];
     std::uint16_t* kc = kc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
     std::uint16_t* vc = vc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
-    RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
-    gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
+    if (fused(L.wqkv, T)) {
+      RH_CHECK(rh_gemv_f16_rmsnorm(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, QKV, 0.0f, stream_));
+    } else {
+      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
+    }
     RH_CHECK(rh_qkv_post(qkv_.p, T, L.bqkv.n ? L.bqkv.p : nullptr, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc,
                          fast_attention_ ? qh_.p : nullptr, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
@@ -478,10 +488,19 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
                                       c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
     }
     gemm(L.wo, attn_.p, x_.p, T, 1.0f);  // x += attn W_o^T
-    RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
-    gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
-    RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
-    gemm(L.w_down, act_.p, x_.p, T, 1.0f);  // x += act W_down^T
+    if (fused(L.w_gate_up, T)) {
+      RH_CHECK(rh_gemv_f16_rmsnorm(L.w_gate_up.f16.p, H, x_.p, L.mlp_norm.p, eps, gu_.p, T, H, 2 * I, 0.0f,
+                                   stream_));
+    } else {
+      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
+      gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
+    }
+    if (fused(L.w_down, T)) {
+      RH_CHECK(rh_gemv_f16_silu(L.w_down.f16.p, I, gu_.p, x_.p, T, I, H, 1.0f, stream_));  // x += act W_down^T
+    } else {
+      RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
+      gemm(L.w_down, act_.p, x_.p, T, 1.0f);  // x += act W_down^T
+    }
   }
   std::vector<float> out(static_cast<std::size_t>(R) * V);
   if (R) {

@@ -73,3 +73,55 @@ def test_rejects_bad_shapes(torch_mod, dev):
     assert L.rh_gemv_f16(None, 72, None, None, 1, 72, 64, 0.0, None) != 0 and "K must" in _lib.last_error()
     assert L.rh_gemv_f16(None, 60, None, None, 1, 64, 64, 0.0, None) != 0 and "ldw" in _lib.last_error()
     assert L.rh_gemv_f16_max_tokens() == 32
+
+
+# Fused producers: rh_gemv_f16_rmsnorm / rh_gemv_f16_silu must give the same bits as the
+# two-launch chain they replace (rh_rmsnorm or rh_silu_mul, then rh_gemv_f16), whose parts
+# are checked against their own references (test_layer_ops.py and the tests above).
+def _chain_and_fused(torch, dev, kind, T, K, N, beta, seed):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    rng = np.random.default_rng(seed)
+    W = torch.from_numpy((rng.standard_normal((N, K)) * 0.05).astype(np.float16).view(np.int16)).to(dev)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    want = torch.from_numpy(y0.copy()).to(dev)
+    got = torch.from_numpy(y0.copy()).to(dev)
+    xh = torch.empty((T, K), dtype=torch.int16, device=dev)
+    print(f"gemv_f16 fused {kind}: T={T} K={K} N={N} beta={beta}", flush=True)
+    if kind == "rmsnorm":
+        x = torch.from_numpy((rng.standard_normal((T, K)) * 3).astype(np.float32)).to(dev)
+        nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).to(dev)
+        _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), K, 1e-5, xh.data_ptr(), None), "rh_rmsnorm")
+        _lib.check(L.rh_gemv_f16_rmsnorm(W.data_ptr(), K, x.data_ptr(), nw.data_ptr(), 1e-5, got.data_ptr(), T, K, N,
+                                         beta, None), "rh_gemv_f16_rmsnorm")
+    else:
+        gu = torch.from_numpy((rng.standard_normal((T, 2 * K)) * 2).astype(np.float32)).to(dev)
+        _lib.check(L.rh_silu_mul(gu.data_ptr(), T, K, xh.data_ptr(), None), "rh_silu_mul")
+        _lib.check(L.rh_gemv_f16_silu(W.data_ptr(), K, gu.data_ptr(), got.data_ptr(), T, K, N, beta, None),
+                   "rh_gemv_f16_silu")
+    _lib.check(L.rh_gemv_f16(W.data_ptr(), K, xh.data_ptr(), want.data_ptr(), T, K, N, beta, None), "rh_gemv_f16")
+    torch.cuda.synchronize()
+    return want.cpu().numpy(), got.cpu().numpy()
+
+
+@pytest.mark.parametrize("kind", ["rmsnorm", "silu"])
+@pytest.mark.parametrize("T,K,N,beta", [(1, 576, 960, 0.0), (16, 576, 3072, 0.0), (7, 1536, 576, 1.0),
+                                        (32, 960, 100, 0.0), (3, 4096, 512, 1.0), (2, 14336, 256, 1.0),
+                                        (17, 48, 33, 0.0)])
+def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta):
+    from relay_amd import _lib
+
+    assert _lib.lib().rh_gemv_f16_fused_fits(T, K)
+    want, got = _chain_and_fused(torch_mod, dev, kind, T, K, N, beta, seed=T + K + N)
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
+
+
+def test_fused_limits(torch_mod, dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_f16_fused_fits(16, 2040) and not L.rh_gemv_f16_fused_fits(16, 2048)
+    assert L.rh_gemv_f16_fused_fits(2, 14336) and not L.rh_gemv_f16_fused_fits(33, 16)
+    assert L.rh_gemv_f16_silu(None, 2048, None, None, 16, 2048, 64, 0.0, None) != 0
+    assert "LDS" in _lib.last_error()
