@@ -162,6 +162,16 @@ int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, in
                      void* stream);
 int rh_gemv_f16_fused_fits(int T, int K);
 
+/* rh_gemv_f16_rmsnorm of the fused qkv projection (N = (heads + 2 kv_heads) head_dim) with
+ * rh_qkv_post folded in as its epilogue: qkv fp32 [T, N] gets the same values, k and v rows
+ * go into the paged cache and q to q_out (may be NULL) exactly as rh_qkv_post writes them
+ * (relay runs rms_norm, the GEMM and qkv_post as three launches, cuda_backend.cu:575-578).
+ * head_dim a multiple of 16; the limits of rh_gemv_f16_rmsnorm. */
+int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
+                            float* qkv, int T, int K, const float* bias, const float* inv_freq, const int* pos,
+                            const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
+                            void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream);
+
 /* Largest T rh_gemv_f16 takes. */
 int rh_gemv_f16_max_tokens(void);
 

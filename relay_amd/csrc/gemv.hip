@@ -132,12 +132,84 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
 // saves the separate normalisation / activation launch at decode batch sizes.
 enum Prologue { kPlain = 0, kRmsNorm = 1, kSiluMul = 2 };
 
+// What the fp16 kernel does with its sums: kStore writes y (+ beta y); kRope is the qkv
+// projection's epilogue, relay's qkv_post step folded in (bias, RoPE on q and k heads,
+// k and v into the paged cache as fp16, q as fp16). For kRope the tile of workgroup i
+// holds rows (h D + j0 + r, h D + D/2 + j0 + r), r < 8, of head h = i / (D/16),
+// j0 = 8 (i % (D/16)), so both halves of every RoPE pair end in one wave.
+enum Epilogue { kStore = 0, kRope = 1 };
+
+struct RopeArgs {
+  const float* bias;  // [N] or null
+  const float* inv_freq;
+  const int* pos;
+  const int* seq;
+  const int* table_off;
+  const int* tables;
+  half_t* kc;
+  half_t* vc;
+  half_t* q_out;  // [T, heads * D] or null
+  int heads, kv_heads, D, block_size;
+};
+
+__device__ __forceinline__ int rope_tile_row(int tile, int m, int D) {
+  const int tph = D / 16, h = tile / tph, j0 = (tile - h * tph) * 8;
+  return h * D + (m < 8 ? j0 + m : D / 2 + j0 + m - 8);
+}
+
+// Lane (c, g) of wave 0 holds token t's sums for tile rows m = 4g + r; the pair of row m
+// (m < 8) is row m + 8, held by lane (c, g + 2). The same float operations as qkv_post
+// (bias add, then a cs - b sn / b cs + a sn, products rounded, sincosf of pos * inv_freq[i]).
+__device__ __forceinline__ void rope_epilogue(const RopeArgs& ra, const float (&s)[4], int tile, int g, int t,
+                                              bool live, float* qkv, int N) {
+  const int D = ra.D, tph = D / 16, h = tile / tph, j0 = (tile - h * tph) * 8;
+  const bool first = g < 2;
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = rope_tile_row(tile, 4 * g + r, D);
+    v[r] = ra.bias ? s[r] + ra.bias[n] : s[r];
+  }
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] = __shfl_xor(v[r], 32);  // every lane takes part
+  if (!live) return;
+  const int p = ra.pos[t];
+  const bool rotate = h < ra.heads + ra.kv_heads;
+  int64_t kv_base = 0;
+  if (h >= ra.heads) {
+    const int block = ra.tables[ra.table_off[ra.seq[t]] + p / ra.block_size];
+    kv_base = kv_row_offset(block, ra.kv_heads, (h - ra.heads) % ra.kv_heads, ra.block_size, p % ra.block_size, D);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * g + r, j = m < 8 ? j0 + m : D / 2 + j0 + m - 8;
+    float out = v[r];
+    if (rotate) {
+      const float angle = static_cast<float>(p) * ra.inv_freq[j0 + (m & 7)];
+      float sn, cs;
+      sincosf(angle, &sn, &cs);
+      out = first ? __fsub_rn(__fmul_rn(v[r], cs), __fmul_rn(o[r], sn))
+                  : __fadd_rn(__fmul_rn(v[r], cs), __fmul_rn(o[r], sn));
+    }
+    qkv[static_cast<int64_t>(t) * N + h * D + j] = out;
+    if (h < ra.heads) {
+      if (ra.q_out) ra.q_out[static_cast<int64_t>(t) * ra.heads * D + h * D + j] = static_cast<half_t>(out);
+    } else if (h < ra.heads + ra.kv_heads) {
+      ra.kc[kv_base + j] = static_cast<half_t>(out);
+    } else {
+      ra.vc[kv_base + j] = static_cast<half_t>(out);
+    }
+  }
+}
+
 // fp16 weights, T <= 16 * NB tokens (NB column blocks of 16 tokens share each A operand).
-template <int WAVES, int NB, int PRO>
+template <int WAVES, int NB, int PRO, int EPI>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* __restrict__ wt, int64_t ldw,
                                                                  const void* __restrict__ xin,
                                                                  const float* __restrict__ norm_w, float eps,
-                                                                 float* y, int T, int K, int N, float beta) {
+                                                                 float* y, int T, int K, int N, float beta,
+                                                                 RopeArgs ra) {
   __shared__ float red[WAVES][NB][kWave * 4];
   __shared__ float s_inv[2 * kMaxTokens];
   extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
@@ -145,7 +217,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
-  const int row = min(n0 + c, N - 1);
+  const int row = EPI == kRope ? rope_tile_row(blockIdx.x, c, ra.D) : min(n0 + c, N - 1);
   const int nchunks = (K + kChunk - 1) / kChunk;
   const int per = (nchunks + WAVES - 1) / WAVES;
   const int cb = w * per, ce = min(nchunks, cb + per);
@@ -159,6 +231,18 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   const int XR = K + 8;
+  // The first batch of weight loads goes out before the prologue, which does not need it.
+  half8 wa[kUnroll], wb[kUnroll];
+  auto load_w = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int k = (q0 + u) * kChunk + 16 * g;
+      const bool live = q0 + u < ce && k < K;
+      wa[u] = live ? load_half8(wrow + k) : zero;
+      wb[u] = live ? load_half8(wrow + k + 8) : zero;
+    }
+  };
+  load_w(cb);
   if (PRO == kRmsNorm) {
     const float* xf = static_cast<const float*>(xin);
     for (int t = w; t < T; t += WAVES) {
@@ -189,13 +273,11 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   for (int q0 = cb; q0 < ce; q0 += kUnroll) {
-    half8 wa[kUnroll], wb[kUnroll], xa[NB][kUnroll], xb[NB][kUnroll];
+    half8 xa[NB][kUnroll], xb[NB][kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int k = (q0 + u) * kChunk + 16 * g;
       const bool live = q0 + u < ce && k < K;
-      wa[u] = live ? load_half8(wrow + k) : zero;
-      wb[u] = live ? load_half8(wrow + k + 8) : zero;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         if (PRO == kPlain) {
@@ -216,6 +298,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
         acc[b] = mfma16x16x32(wa[u], xa[b][u], acc[b]);
         acc[b] = mfma16x16x32(wb[u], xb[b][u], acc[b]);
       }
+    if (q0 + kUnroll < ce) load_w(q0 + kUnroll);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -231,6 +314,10 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     for (int ww = 0; ww < WAVES; ++ww)
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[r] += red[ww][b][lane * 4 + r];
+    if (EPI == kRope) {
+      rope_epilogue(ra, s, blockIdx.x, g, 16 * b + c, tok[b], y, N);
+      continue;
+    }
     if (!tok[b]) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -284,9 +371,9 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
 
 extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
 
-template <int PRO>
+template <int PRO, int EPI = kStore>
 static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const float* norm_w, float eps, float* y,
-                           int T, int K, int N, float beta, void* stream) {
+                           int T, int K, int N, float beta, void* stream, const RopeArgs& ra = RopeArgs{}) {
   RH_REQUIRE(T >= 1 && T <= 2 * kMaxTokens, "gemv_f16: T must be in 1..32");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_f16: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
@@ -299,8 +386,8 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   const int tiles = (N + 15) / 16;
   const bool wide = tiles < 256;
 #define RH_GEMV_F16(W, NBLK)                                                                                    \
-  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO>), dim3(tiles), dim3(W * kWave), lds, s, wt, ldw, \
-                                   x, norm_w, eps, y, T, K, N, beta))
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles), dim3(W * kWave), lds, s, wt, \
+                                   ldw, x, norm_w, eps, y, T, K, N, beta, ra))
   if (T <= kMaxTokens) {
     if (wide) {
       RH_GEMV_F16(16, 1);
@@ -330,6 +417,22 @@ extern "C" int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x,
 extern "C" int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N,
                                 float beta, void* stream) {
   return gemv_f16_launch<kSiluMul>(w16, ldw, gu, nullptr, 0.0f, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
+                                       float* qkv, int T, int K, const float* bias, const float* inv_freq,
+                                       const int* pos, const int* seq, const int* table_off, const int* tables,
+                                       void* kpool, void* vpool, void* q_out, int heads, int kv_heads, int head_dim,
+                                       int block_size, void* stream) {
+  RH_REQUIRE(norm_w != nullptr && inv_freq && pos && seq && table_off && tables && kpool && vpool,
+             "gemv_f16_rmsnorm_qkv: missing pointer");
+  RH_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gemv_f16_rmsnorm_qkv: bad head counts");
+  RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "gemv_f16_rmsnorm_qkv: head_dim must be a multiple of 16");
+  RH_REQUIRE(block_size > 0, "gemv_f16_rmsnorm_qkv: bad block size");
+  RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
+              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  return gemv_f16_launch<kRmsNorm, kRope>(w16, ldw, x, norm_w, eps, qkv, T, K, N, 0.0f, stream, ra);
 }
 
 extern "C" int rh_gemv_f16_fused_fits(int T, int K) {

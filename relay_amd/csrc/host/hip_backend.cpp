@@ -465,14 +465,19 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     DeviceLayer& L = layers_[l];
     std::uint16_t* kc = kc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
     std::uint16_t* vc = vc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
-    if (fused(L.wqkv, T)) {
-      RH_CHECK(rh_gemv_f16_rmsnorm(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, QKV, 0.0f, stream_));
+    const float* bias = L.bqkv.n ? L.bqkv.p : nullptr;
+    std::uint16_t* q_out = fast_attention_ ? qh_.p : nullptr;
+    if (fused(L.wqkv, T) && D % 16 == 0) {
+      // RMSNorm, the projection and qkv_post in one launch.
+      RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
+                                       d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
+                                       layout_.block_size, stream_));
     } else {
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
+      RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads,
+                           c_.kv_heads, D, layout_.block_size, stream_));
     }
-    RH_CHECK(rh_qkv_post(qkv_.p, T, L.bqkv.n ? L.bqkv.p : nullptr, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc,
-                         fast_attention_ ? qh_.p : nullptr, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
     if (observer) observer->kv_written(l);
     if (fast_attention_) {

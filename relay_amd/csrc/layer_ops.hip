@@ -88,10 +88,12 @@ __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_
     const int h = idx / half, i = idx % half;
     float* v = row + h * D;  // q heads, then the k heads that follow them
     const float angle = static_cast<float>(p) * inv_freq[i];
-    const float cs = cosf(angle), sn = sinf(angle);
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
     const float a = v[i], b = v[i + half];
-    v[i] = a * cs - b * sn;
-    v[i + half] = b * cs + a * sn;
+    // Products rounded before the add (no fused multiply-add), as the CPU computes them.
+    v[i] = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+    v[i + half] = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < KV; idx += kThreads) {

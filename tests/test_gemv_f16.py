@@ -125,3 +125,68 @@ def test_fused_limits(torch_mod, dev):
     assert L.rh_gemv_f16_fused_fits(2, 14336) and not L.rh_gemv_f16_fused_fits(33, 16)
     assert L.rh_gemv_f16_silu(None, 2048, None, None, 16, 2048, 64, 0.0, None) != 0
     assert "LDS" in _lib.last_error()
+
+
+@pytest.mark.parametrize("T,heads,kvh,D,H,bs,with_bias", [(1, 9, 3, 64, 576, 16, False), (15, 32, 4, 64, 2048, 16, True),
+                                                         (5, 32, 8, 128, 4096, 16, False), (20, 8, 2, 64, 320, 12, True),
+                                                         (3, 4, 4, 16, 64, 1, True)])
+def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias):
+    """rh_gemv_f16_rmsnorm_qkv against rh_rmsnorm -> rh_gemv_f16 -> rh_qkv_post.
+    Without rotation (inv_freq = 0) every byte of qkv, q and both caches is equal: same sums,
+    same placement. With RoPE the two kernels' inlined sincosf/products round differently in
+    the last bit (measured: ~20% of rotated values 1 ulp apart), so rotated fp32 values must
+    agree within 4 ulp of the pair's magnitude and fp16 values within 1 ulp."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(T * 31 + D + H)
+    N = (heads + 2 * kvh) * D
+    assert L.rh_gemv_f16_fused_fits(T, H)
+    pos = [int(p) for p in rng.permutation(5 * bs + 3)[:T]]  # distinct: one writer per cache slot
+    seq = [t % 2 for t in range(T)]
+    per = (5 * bs + 3) // bs + 1
+    nblocks = 2 * per + 3
+    tables = [int(b) for b in rng.permutation(nblocks)[:2 * per]]
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    W = dt((rng.standard_normal((N, H)) * 0.05).astype(np.float16).view(np.int16))
+    x = dt((rng.standard_normal((T, H)) * 2).astype(np.float32))
+    nw = dt(rng.uniform(0.5, 1.5, H).astype(np.float32))
+    bias = dt(rng.standard_normal(N).astype(np.float32)) if with_bias else None
+    P, S = dt(np.array(pos, np.int32)), dt(np.array(seq, np.int32))
+    TO, TB = dt(np.array([0, per], np.int32)), dt(np.array(tables, np.int32))
+    bp = bias.data_ptr() if bias is not None else None
+
+    def run(fused, inv):
+        kc = torch.full((nblocks * kvh * bs * D,), 0x7BFF, dtype=torch.int16, device=dev)
+        vc = kc.clone()
+        qo = torch.zeros(T * heads * D, dtype=torch.int16, device=dev)
+        qkv = torch.full((T, N), float("nan"), device=dev)
+        if fused:
+            _lib.check(L.rh_gemv_f16_rmsnorm_qkv(W.data_ptr(), H, x.data_ptr(), nw.data_ptr(), 1e-5, qkv.data_ptr(), T, H,
+                                                 bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
+                                                 TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh,
+                                                 D, bs, None), "rh_gemv_f16_rmsnorm_qkv")
+        else:
+            xn = torch.empty((T, H), dtype=torch.int16, device=dev)
+            _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
+            _lib.check(L.rh_gemv_f16(W.data_ptr(), H, xn.data_ptr(), qkv.data_ptr(), T, H, N, 0.0, None), "rh_gemv_f16")
+            _lib.check(L.rh_qkv_post(qkv.data_ptr(), T, bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
+                                     TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs,
+                                     None), "rh_qkv_post")
+        torch.cuda.synchronize()
+        return [a.cpu().numpy() for a in (qkv, kc, vc, qo)]
+
+    print(f"fused qkv: T={T} heads={heads}/{kvh} D={D} H={H} bs={bs} bias={with_bias}", flush=True)
+    inv0 = dt(np.zeros(D // 2, np.float32))
+    for name, a, b in zip(("qkv", "k cache", "v cache", "q"), run(False, inv0), run(True, inv0)):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+    inv = dt((1.0 / 10000.0 ** (np.arange(0, D, 2) / D)).astype(np.float32))
+    (qa, ka, va, oa), (qb, kb, vb, ob) = run(False, inv), run(True, inv)
+    # fp32: the magnitude of a rotated value is bounded by |a| + |b| of its pair
+    pair = np.abs(qa.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True)
+    bound = 4 * 2.0 ** -24 * np.broadcast_to(pair, (T, N // D, 2, D // 2)).reshape(T, N)
+    assert (np.abs(qa - qb) <= bound).all()
+    for name, a, b in (("k cache", ka, kb), ("v cache", va, vb), ("q", oa, ob)):
+        diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
+        assert diff.max() <= 1 and (np.sign(a) == np.sign(b)).all(), name
