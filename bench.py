@@ -275,7 +275,8 @@ def bench_llama3_mixed(steps, int8=False, n_dec=48, ctx=8192, chunk=512):
     for r in range(steps + 2):
         seqs = [SeqChunk([int(rng.integers(c.vocab))], ctx - 1, list(range(i * per, (i + 1) * per)), True)
                 for i in range(n_dec)]
-        seqs.append(SeqChunk(rng.integers(0, c.vocab, size=chunk).tolist(), 0, ptable, True))
+        if chunk:
+            seqs.append(SeqChunk(rng.integers(0, c.vocab, size=chunk).tolist(), 0, ptable, True))
         t0 = time.perf_counter()
         be.forward(ForwardBatch(seqs))
         wall = (time.perf_counter() - t0) * 1e3
@@ -344,7 +345,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3", "tinyllama"],
+    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
+                                           "llama3decint8", "tinyllama"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
@@ -382,8 +384,9 @@ def main():
             r = bench_config1()
         elif args.leg == "tinyllama":
             r = bench_tinyllama_decode(args.steps)
-        else:
-            r = bench_llama3_mixed(args.steps)
+        elif args.leg.startswith("llama3"):
+            r = bench_llama3_mixed(args.steps, int8=args.leg.endswith("int8"),
+                                   chunk=0 if args.leg.startswith("llama3dec") else 512)
         print(json.dumps({"leg": args.leg, **r}), flush=True)
         return
 

@@ -175,6 +175,16 @@ int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const 
 /* Largest T rh_gemv_f16 takes. */
 int rh_gemv_f16_max_tokens(void);
 
+/* y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), any T >= 0:
+ * the weight-only int8 product above the GEMV's token limit, on the matrix cores with the
+ * int8 weights read once. W8 [N, K] rows ldw bytes apart (ldw >= K, a multiple of 16),
+ * scale fp32 [N], x fp16 [T, K], y fp32 [T, N]; K a multiple of 64; W8 and x 16-byte
+ * aligned. Same function as rh_gemv_int8 (fp32 sums of exact products, then the scale).
+ * Replaces relay's dequantize + cublasGemmEx for T above the GEMV limit
+ * (cuda_backend.cu:718-722). */
+int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
+               float beta, void* stream);
+
 /* Per-row symmetric int8 quantization of an fp32 matrix [N, K] on the device:
  * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale),
  * q rows ldq bytes apart (ldq >= K; the bytes past K are not written).

@@ -58,6 +58,7 @@ SIGNATURES = {
     "rh_gemv_int8_row_stride": (I64, [I]),
     "rh_gemv_f16": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_max_tokens": (I, []),
+    "rh_gemm_w8": (I, [P, I64, P, P, P, I, I, I, F, P]),
     "rh_gemv_f16_rmsnorm": (I, [P, I64, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_f16_silu": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_fused_fits": (I, [I, I]),

@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "librelay_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["decode_attention.hip", "flash_prefill.hip", "gemv.hip", "layer_ops.hip"]
+HIP_SOURCES = ["decode_attention.hip", "flash_prefill.hip", "gemv.hip", "gemm_w8.hip", "layer_ops.hip"]
 HOST_SOURCES = ["host/hip_backend.cpp", "host/capi.cpp", "host/config.cpp", "host/backend_defaults.cpp"]
 
 HIPCC_FLAGS = [

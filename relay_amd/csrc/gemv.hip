@@ -38,6 +38,7 @@ namespace relay_hip {
 namespace {
 
 constexpr int kMaxTokens = 16;
+constexpr int kMaxInt8Tokens = 64;
 constexpr size_t kFusedLdsBytes = 64 << 10;  // staged activations of the fused fp16 products
 constexpr int kChunk = 64;   // k per wave step
 constexpr int kUnroll = 4;   // chunks whose loads are issued together
@@ -55,12 +56,15 @@ __device__ __forceinline__ half8 int8x8_to_half8(uint32_t lo, uint32_t hi) {
   return v - bias;
 }
 
-template <int WAVES, bool F16_SCALE>
+// T <= 16 * NB tokens: NB column blocks of 16 tokens share each converted A operand. Fewer
+// chunks per load batch as NB grows keeps the activation operands in registers.
+template <int WAVES, int NB, bool F16_SCALE>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                   const void* __restrict__ scale,
                                                                   const half_t* __restrict__ x, float* y, int T,
                                                                   int K, int N, float beta) {
-  __shared__ float red[WAVES][kWave * 4];
+  constexpr int U = NB == 1 ? kUnroll : (NB == 2 ? 2 : 1);
+  __shared__ float red[WAVES][NB][kWave * 4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
@@ -69,57 +73,68 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   const int per = (nchunks + WAVES - 1) / WAVES;
   const int cb = w * per, ce = min(nchunks, cb + per);
   const int8_t* wrow = w8 + static_cast<int64_t>(row) * ldw;
-  const bool tok = c < T;
-  const half_t* xrow = x + static_cast<int64_t>(tok ? c : 0) * K;
-
-  float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int q0 = cb; q0 < ce; q0 += kUnroll) {
-    uint4v wv[kUnroll];
-    half8 xa[kUnroll], xb[kUnroll];
+  bool tok[NB];
+  const half_t* xrow[NB];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+  for (int b = 0; b < NB; ++b) {
+    tok[b] = 16 * b + c < T;
+    xrow[b] = x + static_cast<int64_t>(tok[b] ? 16 * b + c : 0) * K;
+  }
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+
+  float4v acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = cb; q0 < ce; q0 += U) {
+    uint4v wv[U];
+    half8 xa[NB][U], xb[NB][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
       const int k = (q0 + u) * kChunk + 16 * g;
       const bool live = q0 + u < ce && k < K;
       wv[u] = live ? *reinterpret_cast<const uint4v*>(wrow + k) : uint4v{0u, 0u, 0u, 0u};
-      if (live && tok) {
-        xa[u] = load_half8(xrow + k);
-        xb[u] = load_half8(xrow + k + 8);
-      } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          xa[u][e] = 0;
-          xb[u][e] = 0;
-        }
+      for (int b = 0; b < NB; ++b) {
+        xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
+        xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const half8 a0 = int8x8_to_half8(wv[u][0], wv[u][1]);
       const half8 a1 = int8x8_to_half8(wv[u][2], wv[u][3]);
-      acc = mfma16x16x32(a0, xa[u], acc);
-      acc = mfma16x16x32(a1, xb[u], acc);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        acc[b] = mfma16x16x32(a0, xa[b][u], acc[b]);
+        acc[b] = mfma16x16x32(a1, xb[b][u], acc[b]);
+      }
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) red[w][lane * 4 + r] = acc[r];
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][b][lane * 4 + r] = acc[b][r];
   __syncthreads();
   if (w != 0) return;
-  // Lane (c, g) now sums the waves for token c, rows n0 + 4g + r.
-  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int ww = 0; ww < WAVES; ++ww)
+  for (int b = 0; b < NB; ++b) {
+    // Lane (c, g) now sums the waves for token 16b + c, rows n0 + 4g + r, in a fixed order.
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] += red[ww][lane * 4 + r];
-  if (!tok) return;
+    for (int ww = 0; ww < WAVES; ++ww)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int n = n0 + 4 * g + r;
-    if (n >= N) continue;
-    float sc;
-    if (F16_SCALE) sc = static_cast<float>(static_cast<const half_t*>(scale)[n]);
-    else sc = static_cast<const float*>(scale)[n];
-    float* dst = y + static_cast<int64_t>(c) * N + n;
-    *dst = s[r] * sc + (beta != 0.0f ? beta * *dst : 0.0f);
+      for (int r = 0; r < 4; ++r) s[r] += red[ww][b][lane * 4 + r];
+    if (!tok[b]) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = n0 + 4 * g + r;
+      if (n >= N) continue;
+      float sc;
+      if (F16_SCALE) sc = static_cast<float>(static_cast<const half_t*>(scale)[n]);
+      else sc = static_cast<const float*>(scale)[n];
+      float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+      *dst = s[r] * sc + (beta != 0.0f ? beta * *dst : 0.0f);
+    }
   }
 }
 
@@ -329,18 +344,27 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
 }
 
-template <bool F16_SCALE>
-int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
-           float beta, hipStream_t s) {
+template <int NB, bool F16_SCALE>
+int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
+              float beta, hipStream_t s) {
   const int tiles = (N + 15) / 16;
   if (tiles < 256) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s, w8,
-                                     ldw, scale, x, y, T, K, N, beta));
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, NB, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s,
+                                     w8, ldw, scale, x, y, T, K, N, beta));
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s, w8,
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, NB, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s, w8,
                                      ldw, scale, x, y, T, K, N, beta));
   }
   return 0;
+}
+
+template <bool F16_SCALE>
+int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
+           float beta, hipStream_t s) {
+  if (T <= 16) return launch_nb<1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  if (T <= 32) return launch_nb<2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  if (T <= 48) return launch_nb<3, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  return launch_nb<4, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
 }
 
 }  // namespace
@@ -348,7 +372,7 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 
 using namespace relay_hip;
 
-extern "C" int rh_gemv_int8_max_tokens(void) { return kMaxTokens; }
+extern "C" int rh_gemv_int8_max_tokens(void) { return kMaxInt8Tokens; }
 
 extern "C" int64_t rh_gemv_int8_row_stride(int K) {
   if (K <= 0) return -1;
@@ -358,7 +382,7 @@ extern "C" int64_t rh_gemv_int8_row_stride(int K) {
 
 extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
                             float* y, int T, int K, int N, float beta, void* stream) {
-  RH_REQUIRE(T >= 1 && T <= kMaxTokens, "gemv_int8: T must be in 1..16");
+  RH_REQUIRE(T >= 1 && T <= kMaxInt8Tokens, "gemv_int8: T must be in 1..64");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemv_int8: ldw must be >= K and a multiple of 16");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,

@@ -1,0 +1,110 @@
+"""Weight-only int8 GEMM (rh_gemm_w8) against a float64 reference.
+
+y[t, n] = scale[n] * sum_k q[n, k] x[t, k] (+ beta y). The products q * x are exact in fp32,
+so the error is the fp32 accumulation over K terms plus the rounding of the scale multiply
+(and of the beta term): |y - y_exact| <= (4 K 2^-24 + 2^-23) |scale[n]| sum_k |q x| (+ 2^-23
+|beta y|). The exact value is computed in float64 from the same int8/fp16 values (numpy as
+the checker). Sizes cover partial token and row tiles, T above and below the GEMV limit, and
+the shapes of the Llama-3-8B mixed batch (T = 560).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+EPS32 = 2.0 ** -24
+
+
+def make(N, K, T, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    scale = (rng.uniform(0.5, 2.0, N) * 1e-3).astype(np.float32)
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    return q, scale, x
+
+
+def run(torch, dev, q, scale, x, beta=0.0, y0=None, ldw=None):
+    from relay_amd import _lib
+
+    N, K = q.shape
+    T = x.shape[0]
+    ldw = K if ldw is None else ldw
+    padded = np.full((N, ldw), 99, np.int8)
+    padded[:, :K] = q
+    W = torch.from_numpy(padded).to(dev)
+    S = torch.from_numpy(scale).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    Y = torch.from_numpy(y0.copy()).to(dev) if y0 is not None else torch.full((T, N), float("nan"), device=dev)
+    print(f"gemm_w8 case: T={T} K={K} N={N} ldw={ldw} beta={beta}", flush=True)
+    _lib.check(_lib.lib().rh_gemm_w8(W.data_ptr(), ldw, S.data_ptr(), X.data_ptr(), Y.data_ptr(), T, K, N, beta, None),
+               "rh_gemm_w8")
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+def check(y, q, scale, x, beta=0.0, y0=None):
+    qd, xd, sd = q.astype(np.float64), x.astype(np.float64), scale.astype(np.float64)
+    dot = xd @ qd.T
+    mag = (np.abs(xd) @ np.abs(qd).T) * np.abs(sd)
+    exact = dot * sd + (beta * y0.astype(np.float64) if beta else 0.0)
+    bound = (4 * q.shape[1] * EPS32 + 2 * EPS32) * mag + 1e-30
+    if beta:
+        bound = bound + 2 * EPS32 * np.abs(beta * y0.astype(np.float64)) + 2 * EPS32 * np.abs(exact)
+    err = np.abs(y - exact)
+    assert np.isfinite(y).all()
+    assert (err <= bound).all(), f"worst excess {np.max(err - bound):.3e}"
+
+
+@pytest.mark.parametrize("T", [1, 17, 100, 128, 129, 300])
+@pytest.mark.parametrize("N,K", [(64, 64), (100, 128), (576, 1536), (1000, 5632)])
+def test_matches_float64(torch_mod, dev, T, N, K):
+    q, s, x = make(N, K, T, seed=T * 13 + N + K)
+    check(run(torch_mod, dev, q, s, x), q, s, x)
+
+
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 4096), (4096, 14336)])
+def test_llama3_shapes_at_the_mixed_batch(torch_mod, dev, N, K):
+    q, s, x = make(N, K, 560, seed=N + K)
+    check(run(torch_mod, dev, q, s, x), q, s, x)
+
+
+def test_beta_accumulates(torch_mod, dev):
+    q, s, x = make(300, 512, 150, seed=1)
+    y0 = np.random.default_rng(2).standard_normal((150, 300)).astype(np.float32)
+    check(run(torch_mod, dev, q, s, x, beta=1.0, y0=y0), q, s, x, beta=1.0, y0=y0)
+
+
+def test_row_stride_gives_the_same_bits(torch_mod, dev):
+    q, s, x = make(200, 256, 40, seed=3)
+    a = run(torch_mod, dev, q, s, x)
+    b = run(torch_mod, dev, q, s, x, ldw=256 + 272)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_agrees_with_the_gemv_on_its_range(torch_mod, dev):
+    """Both int8 paths compute scale * (fp32 sum of exact products): on T <= 16 they may
+    differ only by accumulation order."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    q, s, x = make(512, 1024, 16, seed=4)
+    a = run(torch, dev, q, s, x)
+    W = torch.from_numpy(q).to(dev)
+    S = torch.from_numpy(s).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    Y = torch.empty((16, 512), device=dev)
+    _lib.check(_lib.lib().rh_gemv_int8(W.data_ptr(), 1024, S.data_ptr(), 0, X.data_ptr(), Y.data_ptr(), 16, 1024, 512,
+                                       0.0, None), "rh_gemv_int8")
+    torch.cuda.synchronize()
+    b = Y.cpu().numpy()
+    mag = (np.abs(x.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * s
+    assert (np.abs(a - b) <= 8 * 1024 * EPS32 * mag + 1e-30).all()
+
+
+def test_rejects_bad_shapes(torch_mod, dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemm_w8(None, 96, None, None, None, 4, 96, 64, 0.0, None) != 0 and "K must" in _lib.last_error()
+    assert L.rh_gemm_w8(None, 72, None, None, None, 4, 64, 64, 0.0, None) != 0 and "ldw" in _lib.last_error()
+    assert L.rh_gemm_w8(None, 64, None, None, None, 0, 64, 64, 0.0, None) == 0  # nothing to do

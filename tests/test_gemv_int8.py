@@ -55,7 +55,7 @@ def bound(w8, scale, x_bits):
     return 4 * K * EPS32 * mag * scale[None, :].astype(np.float64) + 1e-30
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 7, 8, 9, 16])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 7, 8, 9, 16, 17, 32, 33, 48, 64])
 @pytest.mark.parametrize("N,K", [(64, 4096), (1000, 1024), (48, 80), (33, 160), (4096, 576)])
 def test_matches_oracle(torch_mod, dev, T, N, K):
     w8, s, x = make(N, K, T, seed=T * 1000 + N + K)
@@ -80,13 +80,14 @@ def test_fp16_scales(torch_mod, dev):
     assert (np.abs(y - exact) <= bound(w8, s16, x)).all()
 
 
+@pytest.mark.parametrize("T", [8, 48])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
-def test_llama3_shapes(torch_mod, dev, N, K):
-    """BASELINE config 4's projection shapes at T = 8 (fp16 scales), in the padded row
-    layout the backend stores (rh_gemv_int8_row_stride)."""
+def test_llama3_shapes(torch_mod, dev, N, K, T):
+    """BASELINE config 4's projection shapes at T = 8 and at config 5's 48 decode tokens
+    (fp16 scales), in the padded row layout the backend stores (rh_gemv_int8_row_stride)."""
     from relay_amd import _lib
 
-    w8, s, x = make(N, K, 8, seed=N + K)
+    w8, s, x = make(N, K, T, seed=N + K + T)
     s16 = bits_to_f32(f16_bits(s))
     ldw = _lib.lib().rh_gemv_int8_row_stride(K)
     y = run(torch_mod, dev, w8, s, x, f16_scale=True, ldw=ldw)
@@ -106,7 +107,7 @@ def test_row_stride_gives_the_same_bits(torch_mod, dev, ldw):
 def test_rejects_bad_shapes(torch_mod, dev):
     from relay_amd import _lib
 
-    assert _lib.lib().rh_gemv_int8(None, 64, None, 0, None, None, 17, 64, 64, 0.0, None) != 0
+    assert _lib.lib().rh_gemv_int8(None, 64, None, 0, None, None, 65, 64, 64, 0.0, None) != 0
     assert _lib.lib().rh_gemv_int8(None, 72, None, 0, None, None, 1, 72, 64, 0.0, None) != 0
     assert _lib.lib().rh_gemv_int8(None, 48, None, 0, None, None, 1, 64, 64, 0.0, None) != 0
     assert "ldw" in _lib.last_error()

@@ -61,7 +61,7 @@ def test_kernel_launchers_validate_shapes_before_launching():
     assert "T must be" in _lib.last_error()
     assert lib.rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64, None) != 0
     assert lib.rh_prefill_tile_rows() == 128
-    assert lib.rh_gemv_int8_max_tokens() == 16
+    assert lib.rh_gemv_int8_max_tokens() == 64
 
 
 def test_config_parsing_of_the_fixtures():
