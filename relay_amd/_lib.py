@@ -10,7 +10,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librelay_hip.so")
+# RELAY_HIP_LIB selects another build of the library (A/B measurements); default: the in-tree one.
+LIB_PATH = os.environ.get("RELAY_HIP_LIB") or os.path.join(HERE, "librelay_hip.so")
 
 
 class RelayHipError(RuntimeError):

@@ -15,6 +15,11 @@
 // Only the row/column placement matters for correctness: the k slot a (group, register)
 // pair stands for is the same for A and B, so the kernels choose which logical k (key or
 // head dimension) each slot carries, as long as both operands agree.
+//
+// fp16 stores of a product: hipcc turns `(half)(a * b)` into v_fma_mix*_f16, which rounds the
+// exact product once, to fp16 (neither __fmul_rn nor `#pragma clang fp contract(off)` stops
+// it); relay's kernels and its CPU backend round the fp32 product first and then convert,
+// which differs at fp16 ties. f16_of_product keeps the two roundings.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,6 +38,14 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 typedef unsigned int uint4v __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
+
+// fp16(fp32(a * b)): the empty asm makes the rounded fp32 product opaque, so the conversion
+// cannot be fused into a single-rounding v_fma_mix (it emits no instruction).
+__device__ __forceinline__ half_t f16_of_product(float a, float b) {
+  float p = a * b;
+  asm("" : "+v"(p));
+  return static_cast<half_t>(p);
+}
 
 __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

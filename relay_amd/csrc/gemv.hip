@@ -34,6 +34,8 @@
 #include "../../include/relay_hip.h"
 #include "common.h"
 
+#include <algorithm>
+
 namespace relay_hip {
 namespace {
 
@@ -225,9 +227,12 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
                                                                  const float* __restrict__ norm_w, float eps,
                                                                  float* y, int T, int K, int N, float beta,
                                                                  RopeArgs ra) {
-  __shared__ float red[WAVES][NB][kWave * 4];
+  // The cross-wave reduction buffer; with a prologue it reuses the staged activations' LDS
+  // (after a barrier; the launcher sizes that area for both).
+  __shared__ float red_static[PRO == kPlain ? WAVES * NB * kWave * 4 : 1];
   __shared__ float s_inv[2 * kMaxTokens];
   extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
+  float* red = PRO == kPlain ? red_static : reinterpret_cast<float*>(sxb);
   const half_t* x = static_cast<const half_t*>(xin);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
@@ -271,7 +276,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     __syncthreads();
     for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
       const int t = idx / K, i = idx - t * K;
-      sxb[t * XR + i] = static_cast<half_t>(norm_w[i] * (xf[static_cast<int64_t>(t) * K + i] * s_inv[t]));
+      sxb[t * XR + i] = f16_of_product(norm_w[i], xf[static_cast<int64_t>(t) * K + i] * s_inv[t]);
     }
     __syncthreads();
   } else if (PRO == kSiluMul) {
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
       const int t = idx / K, i = idx - t * K;
       const float v = gu[static_cast<int64_t>(t) * 2 * K + i];
-      sxb[t * XR + i] = static_cast<half_t>(v / (1.0f + expf(-v)) * gu[static_cast<int64_t>(t) * 2 * K + K + i]);
+      sxb[t * XR + i] = f16_of_product(v / (1.0f + expf(-v)), gu[static_cast<int64_t>(t) * 2 * K + K + i]);
     }
     __syncthreads();
   }
@@ -315,10 +320,11 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
       }
     if (q0 + kUnroll < ce) load_w(q0 + kUnroll);
   }
+  if (PRO != kPlain) __syncthreads();  // every wave is done reading the staged activations
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[w][b][lane * 4 + r] = acc[b][r];
+    for (int r = 0; r < 4; ++r) red[((w * NB + b) * kWave + lane) * 4 + r] = acc[b][r];
   __syncthreads();
   if (w != 0) return;
 #pragma unroll
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 #pragma unroll
     for (int ww = 0; ww < WAVES; ++ww)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] += red[ww][b][lane * 4 + r];
+      for (int r = 0; r < 4; ++r) s[r] += red[((ww * NB + b) * kWave + lane) * 4 + r];
     if (EPI == kRope) {
       rope_epilogue(ra, s, blockIdx.x, g, 16 * b + c, tok[b], y, N);
       continue;
@@ -403,14 +409,15 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_f16: W16 and x must be 16-byte aligned");
-  const size_t lds = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
-  RH_REQUIRE(lds <= kFusedLdsBytes, "gemv_f16: T * (K + 8) fp16 activations exceed the fused path's LDS");
+  const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
+  RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_f16: T * (K + 8) fp16 activations exceed the fused path's LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* wt = static_cast<const half_t*>(w16);
   const int tiles = (N + 15) / 16;
   const bool wide = tiles < 256;
 #define RH_GEMV_F16(W, NBLK)                                                                                    \
-  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles), dim3(W * kWave), lds, s, wt, \
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles), dim3(W * kWave),             \
+                                   PRO == kPlain ? 0 : std::max<size_t>(staged, W * NBLK * kWave * 4 * sizeof(float)), s, wt, \
                                    ldw, x, norm_w, eps, y, T, K, N, beta, ra))
   if (T <= kMaxTokens) {
     if (wide) {

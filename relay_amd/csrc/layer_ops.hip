@@ -70,7 +70,43 @@ __global__ void rmsnorm_kernel(const float* x, const int* rows, const float* w, 
   ss = block_sum(ss, scratch);
   const float inv = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
   for (int i = threadIdx.x; i < H; i += kThreads)
-    out[static_cast<int64_t>(r) * H + i] = static_cast<half_t>(w[i] * (xr[i] * inv));
+    out[static_cast<int64_t>(r) * H + i] = f16_of_product(w[i], xr[i] * inv);
+}
+
+// Rows of H <= 4 * 4 * kThreads (H % 4 == 0): every x and w load of the row is issued at
+// once as float4s held in registers, then one reduction; same sum of squares in double and
+// the same output expression as rmsnorm_kernel (the summation order differs).
+constexpr int kRmsVec = 4;  // float4 loads per thread
+__global__ void rmsnorm_vec_kernel(const float* x, const int* rows, const float* w, int H, float eps, half_t* out) {
+  __shared__ double scratch[kThreads / 64];
+  const int r = blockIdx.x;
+  const float4* xr = reinterpret_cast<const float4*>(x + static_cast<int64_t>(rows ? rows[r] : r) * H);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  const int n4 = H / 4;
+  float4 xv[kRmsVec], wv[kRmsVec];
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int j = threadIdx.x + i * kThreads;
+    xv[i] = j < n4 ? xr[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    wv[i] = j < n4 ? wr[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  double ss = 0;
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i)
+    ss += static_cast<double>(xv[i].x) * xv[i].x + static_cast<double>(xv[i].y) * xv[i].y +
+          static_cast<double>(xv[i].z) * xv[i].z + static_cast<double>(xv[i].w) * xv[i].w;
+  ss = block_sum(ss, scratch);
+  const float inv = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
+  half4* o = reinterpret_cast<half4*>(out + static_cast<int64_t>(r) * H);
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int j = threadIdx.x + i * kThreads;
+    if (j < n4)
+      o[j] = half4{f16_of_product(wv[i].x, xv[i].x * inv),
+                   f16_of_product(wv[i].y, xv[i].y * inv),
+                   f16_of_product(wv[i].z, xv[i].z * inv),
+                   f16_of_product(wv[i].w, xv[i].w * inv)};
+  }
 }
 
 __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_freq, const int* pos, const int* seq,
@@ -112,8 +148,23 @@ __global__ void silu_mul_kernel(const float* gu, int I, half_t* act) {
   const float* u = g + I;
   for (int i = threadIdx.x; i < I; i += kThreads) {
     const float v = g[i];
-    act[static_cast<int64_t>(t) * I + i] = static_cast<half_t>(v / (1.0f + expf(-v)) * u[i]);
+    act[static_cast<int64_t>(t) * I + i] = f16_of_product(v / (1.0f + expf(-v)), u[i]);
   }
+}
+
+// 8 consecutive elements per thread, blockIdx.y over 2048-element pieces of a row (I % 8 == 0).
+__global__ void silu_mul_vec_kernel(const float* gu, int I, half_t* act) {
+  const int t = blockIdx.x, i = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  if (i >= I) return;
+  const float4* g = reinterpret_cast<const float4*>(gu + static_cast<int64_t>(t) * 2 * I + i);
+  const float4* u = reinterpret_cast<const float4*>(gu + static_cast<int64_t>(t) * 2 * I + I + i);
+  const float4 g0 = g[0], g1 = g[1], u0 = u[0], u1 = u[1];
+  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  half8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = f16_of_product(gv[e] / (1.0f + expf(-gv[e])), uv[e]);
+  *reinterpret_cast<half8*>(act + static_cast<int64_t>(t) * I + i) = r;
 }
 
 __global__ void kv_gather_kernel(const uint4v* k, const uint4v* v, const int* blocks, int n, int64_t vecs, uint4v* out) {
@@ -149,7 +200,7 @@ __global__ void dequant_int8_kernel(const int8_t* w8, int64_t ldw, const float* 
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t n = i / K;
-    out[i] = static_cast<half_t>(static_cast<float>(w8[n * ldw + (i - n * K)]) * scale[n]);
+    out[i] = f16_of_product(static_cast<float>(w8[n * ldw + (i - n * K)]), scale[n]);
   }
 }
 
@@ -259,8 +310,10 @@ int rh_embed(const int* tokens, int T, const void* table, int H, float* x, void*
 int rh_rmsnorm(const float* x, const int* rows, int R, const float* w, int H, float eps, void* out, void* stream) {
   if (R == 0) return 0;
   RH_REQUIRE(R > 0 && H > 0, "rmsnorm: bad shape");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(rmsnorm_kernel, dim3(R), dim3(kThreads), 0, static_cast<hipStream_t>(stream), x,
-                                   rows, w, H, eps, static_cast<half_t*>(out)));
+  const bool vec = H % 4 == 0 && H <= 4 * kRmsVec * kThreads &&
+                   (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(vec ? rmsnorm_vec_kernel : rmsnorm_kernel, dim3(R), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), x, rows, w, H, eps, static_cast<half_t*>(out)));
   return 0;
 }
 
@@ -280,8 +333,14 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
 int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream) {
   if (T == 0) return 0;
   RH_REQUIRE(T > 0 && I > 0, "silu_mul: bad shape");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(silu_mul_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), gu,
-                                   I, static_cast<half_t*>(act)));
+  if (I % 8 == 0 && (reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(act)) % 16 == 0) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(silu_mul_vec_kernel, dim3(T, (I + 8 * kThreads - 1) / (8 * kThreads)),
+                                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), gu, I,
+                                     static_cast<half_t*>(act)));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(silu_mul_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                                     gu, I, static_cast<half_t*>(act)));
+  }
   return 0;
 }
 

@@ -78,7 +78,20 @@ def test_greedy_generation_matches_transformers(dev, model):
 
 @pytest.mark.parametrize("D,heads,kv_heads", [(64, 8, 2), (64, 9, 3), (128, 8, 2), (64, 32, 4)])
 def test_fast_kernels_match_cpu_oracle(dev, D, heads, kv_heads):
+    """GPU vs the fp32 CPU oracle on relay's comparison schedule (test_attention.cpp:43-138) at
+    relay's bar (1e-2). The synthetic weights are rounded to fp16 values first, so the oracle
+    and the GPU see the same weights and the difference measures the GPU arithmetic (fp16
+    activations and attention weights); with fp32 weights the fp16 upload alone puts the
+    32/4-head case at ~1e-2."""
     w = small_model(D, heads, kv_heads, hidden=heads * D // 2)
+    for L in w.layers:
+        for f in ("attn_norm", "wqkv", "bqkv", "wo", "mlp_norm", "w_gate_up", "w_down"):
+            a = getattr(L, f)
+            if a is not None:
+                np.copyto(a, a.astype(np.float16).astype(np.float32))
+    for a in (w.embed, w.lm_head, w.final_norm):
+        if a is not None:
+            np.copyto(a, a.astype(np.float16).astype(np.float32))
     lens = [1, 17, 64, 200, 700, 1300]
     nb = blocks_needed(lens, 12)
     a = O.CpuBackend(w, nb, 16)

@@ -107,7 +107,8 @@ def _chain_and_fused(torch, dev, kind, T, K, N, beta, seed):
 
 @pytest.mark.parametrize("kind", ["rmsnorm", "silu"])
 @pytest.mark.parametrize("T,K,N,beta", [(1, 576, 960, 0.0), (16, 576, 3072, 0.0), (7, 1536, 576, 1.0),
-                                        (32, 960, 100, 0.0), (3, 4096, 512, 1.0), (2, 14336, 256, 1.0),
+                                        (32, 960, 100, 0.0), (3, 4096, 512, 1.0), (2, 14336, 256, 1.0), (5, 5632, 2048, 1.0),
+                                        (16, 2032, 6144, 0.0),
                                         (17, 48, 33, 0.0)])
 def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta):
     from relay_amd import _lib

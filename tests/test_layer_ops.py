@@ -183,3 +183,52 @@ def test_qkv_post_rope_matches_oracle(torch_mod, dev):
             want = np.concatenate([a * cs - b * sn, b * cs + a * sn])
             # angle pos * inv_freq is rounded to fp32 on both sides; cos/sin of it agree to ~1 ulp
             assert np.abs(got[t, h * D:(h + 1) * D] - want).max() <= 4e-6 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("H", [576, 2048, 4096, 102, 8192])
+def test_rmsnorm_bit_exact(torch_mod, dev, H):
+    """out[r] = fp16(w * (x[rows[r]] * inv)), inv = 1 / sqrt(fp32(sum x^2 / H) + eps) with the sum
+    in double (cpu_backend.cpp:47-52); fp32 division and square root are correctly rounded, so
+    numpy reproduces every bit. H = 576..4096 take the vectorised kernel, 102 and 8192 the
+    strided one."""
+    from relay_amd import _lib
+
+    rng = np.random.default_rng(H)
+    R, rows_n = 7, 11
+    x = (rng.standard_normal((rows_n, H)) * rng.uniform(0.1, 30, (rows_n, 1))).astype(np.float32)
+    w = rng.uniform(0.2, 2.0, H).astype(np.float32)
+    rows = rng.permutation(rows_n)[:R].astype(np.int32)
+    eps = np.float32(1e-5)
+    xd = x[rows].astype(np.float64)
+    ss = (xd * xd).sum(axis=1)
+    inv = np.float32(1.0) / np.sqrt((ss / H).astype(np.float32) + eps)
+    want = (w[None, :] * (x[rows] * inv[:, None])).astype(np.float16)
+    dt = lambda a: torch_mod.from_numpy(np.ascontiguousarray(a)).to(dev)
+    X, Wt, RW = dt(x), dt(w), dt(rows)
+    out = torch_mod.empty((R, H), dtype=torch_mod.int16, device=dev)
+    print(f"rmsnorm: H={H}", flush=True)
+    _lib.check(_lib.lib().rh_rmsnorm(X.data_ptr(), RW.data_ptr(), R, Wt.data_ptr(), H, float(eps), out.data_ptr(), None),
+               "rh_rmsnorm")
+    torch_mod.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want.view(np.int16))
+
+
+@pytest.mark.parametrize("T,I", [(1, 1536), (32, 5632), (5, 14336), (3, 100)])
+def test_silu_mul_within_one_fp16_ulp(torch_mod, dev, T, I):
+    """act = fp16(g / (1 + exp(-g)) * u) (cpu_backend.cpp:193): within one fp16 ulp of the
+    float64 value rounded to fp16 (expf is not correctly rounded). I = 100 takes the strided
+    kernel, the others the vectorised one."""
+    from relay_amd import _lib
+
+    rng = np.random.default_rng(T + I)
+    gu = (rng.standard_normal((T, 2 * I)) * 3).astype(np.float32)
+    g, u = gu[:, :I].astype(np.float64), gu[:, I:].astype(np.float64)
+    want = (g / (1 + np.exp(-g)) * u).astype(np.float16)
+    G = torch_mod.from_numpy(gu).to(dev)
+    out = torch_mod.empty((T, I), dtype=torch_mod.int16, device=dev)
+    print(f"silu_mul: T={T} I={I}", flush=True)
+    _lib.check(_lib.lib().rh_silu_mul(G.data_ptr(), T, I, out.data_ptr(), None), "rh_silu_mul")
+    torch_mod.cuda.synchronize()
+    got = out.cpu().numpy().view(np.float16)
+    ulp = np.abs(np.spacing(want.astype(np.float16)).astype(np.float64))
+    assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= ulp + 1e-30).all()
