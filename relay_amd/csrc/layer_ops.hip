@@ -109,37 +109,48 @@ __global__ void rmsnorm_vec_kernel(const float* x, const int* rows, const float*
   }
 }
 
+// One thread per (token, head, pair (i, i + D/2)) of every head, grid (T, pieces): bias, then
+// RoPE on q and k heads, the fp32 row written back, and the fp16 copies (q to q_out, k and v
+// into the paged cache). Each element is touched by one thread, so no barriers.
 __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_freq, const int* pos, const int* seq,
                                 const int* table_off, const int* tables, half_t* kc, half_t* vc, half_t* q_out,
                                 int heads, int kv_heads, int D, int block_size) {
-  const int t = blockIdx.x;
-  const int Q = heads * D, KV = kv_heads * D, QKV = Q + 2 * KV, half = D / 2;
-  float* row = qkv + static_cast<int64_t>(t) * QKV;
-  if (bias)
-    for (int i = threadIdx.x; i < QKV; i += kThreads) row[i] += bias[i];
-  __syncthreads();
+  const int t = blockIdx.x, half = D / 2;
+  const int idx = blockIdx.y * kThreads + threadIdx.x;
+  if (idx >= (heads + 2 * kv_heads) * half) return;
+  const int Q = heads * D, KV = kv_heads * D, QKV = Q + 2 * KV;
+  const int h = idx / half, i = idx % half;
+  float* v = qkv + static_cast<int64_t>(t) * QKV + h * D;  // q heads, then k heads, then v heads
+  float a = v[i], b = v[i + half];
+  if (bias) {
+    a += bias[h * D + i];
+    b += bias[h * D + i + half];
+  }
   const int p = pos[t];
-  const int block = tables[table_off[seq[t]] + p / block_size], slot = p % block_size;
-  for (int idx = threadIdx.x; idx < (heads + kv_heads) * half; idx += kThreads) {
-    const int h = idx / half, i = idx % half;
-    float* v = row + h * D;  // q heads, then the k heads that follow them
+  if (h < heads + kv_heads) {
     const float angle = static_cast<float>(p) * inv_freq[i];
     float sn, cs;
     sincosf(angle, &sn, &cs);
-    const float a = v[i], b = v[i + half];
     // Products rounded before the add (no fused multiply-add), as the CPU computes them.
-    v[i] = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
-    v[i + half] = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
+    const float ra = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+    const float rb = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
+    a = ra;
+    b = rb;
   }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < KV; idx += kThreads) {
-    const int h = idx / D, d = idx % D;
-    const int64_t off = kv_row_offset(block, kv_heads, h, block_size, slot, D) + d;
-    kc[off] = static_cast<half_t>(row[Q + idx]);
-    vc[off] = static_cast<half_t>(row[Q + KV + idx]);
+  v[i] = a;
+  v[i + half] = b;
+  if (h < heads) {
+    if (q_out) {
+      q_out[static_cast<int64_t>(t) * Q + h * D + i] = static_cast<half_t>(a);
+      q_out[static_cast<int64_t>(t) * Q + h * D + i + half] = static_cast<half_t>(b);
+    }
+    return;
   }
-  if (q_out)
-    for (int idx = threadIdx.x; idx < Q; idx += kThreads) q_out[static_cast<int64_t>(t) * Q + idx] = static_cast<half_t>(row[idx]);
+  const int block = tables[table_off[seq[t]] + p / block_size], slot = p % block_size;
+  const int kvh = (h - heads) % kv_heads;
+  half_t* dst = (h < heads + kv_heads ? kc : vc) + kv_row_offset(block, kv_heads, kvh, block_size, slot, D);
+  dst[i] = static_cast<half_t>(a);
+  dst[i + half] = static_cast<half_t>(b);
 }
 
 __global__ void silu_mul_kernel(const float* gu, int I, half_t* act) {
@@ -323,7 +334,9 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
   if (T == 0) return 0;
   RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
              "qkv_post: bad shape");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), qkv,
+  const int pairs = (heads + 2 * kv_heads) * (head_dim / 2);
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), qkv,
                                    bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool),
                                    static_cast<half_t*>(vpool), static_cast<half_t*>(q_out), heads, kv_heads,
                                    head_dim, block_size));
