@@ -48,10 +48,19 @@ class Timer:
     def __init__(self, torch, stream):
         self.torch, self.stream = torch, stream
 
-    def run(self, fn, steps, warmup):
-        for i in range(warmup):
+    def run(self, fn, steps, warmup, min_warm_s=0.25):
+        """At least `warmup` untimed launches, continued until min_warm_s of sustained launches
+        have passed: the GPU's clocks ramp up under load over a few hundred milliseconds, and a
+        handful of 20-40 us launches would otherwise be timed at the idle clock."""
+        t0 = time.perf_counter()
+        i = 0
+        while i < warmup or time.perf_counter() - t0 < min_warm_s:
             fn(i)
+            i += 1
+            if i % 64 == 0:
+                self.torch.cuda.synchronize()
         self.torch.cuda.synchronize()
+        warmup = self.last_warmup = i
         a = self.torch.cuda.Event(enable_timing=True)
         b = self.torch.cuda.Event(enable_timing=True)
         a.record(self.stream)
@@ -178,10 +187,11 @@ def bench_gemv(torch, dev, stream, steps, warmup, Ts=(1, 4, 8)):
                 if rc:
                     raise RuntimeError(_lib.last_error())
 
-            ms = Timer(torch, stream).run(step, steps, warmup)
             algo = N * K + 2 * N + 2 * T * K + 4 * T * N
+            timer = Timer(torch, stream)
+            ms = timer.run(step, steps, warmup)
             res[f"{K}x{N}_T{T}"] = {"us": round(ms * 1e3, 2), "gbs": round(algo / ms / 1e6, 1),
-                                    "frac": round(algo / ms / 1e6 / HBM_PEAK_GBS, 3)}
+                                    "frac": round(algo / ms / 1e6 / HBM_PEAK_GBS, 3), "warmup": timer.last_warmup}
         del ws
         torch.cuda.empty_cache()
     return res
