@@ -47,6 +47,17 @@ __device__ __forceinline__ half_t f16_of_product(float a, float b) {
   return static_cast<half_t>(p);
 }
 
+// ds_read_b64_tr_b16 (gfx950), as measured on MI355X: within each group of 16 lanes, lane i
+// receives element i % 4 of the 8 bytes read by lanes 4j + i / 4 of its group, j = 0..3. So
+// when lane s of a group reads row (r0 + s / 4), columns c0 + 4 (s % 4) .. +3 of a row-major
+// fp16 matrix, lane i receives rows r0 .. r0 + 3 of column c0 + i: the k-major MFMA operand.
+__device__ __forceinline__ half4 tr_read_b64(const half_t* lds_addr) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(const_cast<half_t*>(lds_addr)));
+  return __builtin_bit_cast(half4, v);
+}
+
 __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

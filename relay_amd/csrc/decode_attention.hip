@@ -242,13 +242,14 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
       // O^T += V^T P^T, V^T read column-wise from the staging rows.
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        half8 vt;
-        const int d = 16 * dt + c;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const int kl = r < 4 ? 4 * g + r : 16 + 4 * g + (r - 4);
-          vt[r] = sv[kl * D + ((((d >> 3) ^ vswz(kl))) << 3) + (d & 7)];
-        }
+        // Transposing LDS reads: lane c of group g reads 8 bytes of V row (kb + c / 4),
+        // columns 16 dt + 4 (c % 4) .. +3, and receives V[kb .. kb + 3][16 dt + c]; kb = 4g
+        // and 16 + 4g give the operand's two runs of 4 keys.
+        const int col = 16 * dt + 4 * (c & 3);
+        const int k0r = 4 * g + (c >> 2), k1r = 16 + 4 * g + (c >> 2);
+        const half4 lo = tr_read_b64(sv + k0r * D + (((col >> 3) ^ vswz(k0r)) << 3) + (col & 7));
+        const half4 hi = tr_read_b64(sv + k1r * D + (((col >> 3) ^ vswz(k1r)) << 3) + (col & 7));
+        const half8 vt = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         float4v acc = o[dt];
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] *= alpha;
