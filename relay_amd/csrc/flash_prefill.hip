@@ -24,12 +24,13 @@
 //     sum from the fp16 P values with packed dot products
 //     O^T[D x 32 rows] += V^T[D x 16 keys] * P^T[16 keys x 32 rows]     (D/32 MFMA 32x32x16)
 //   The S^T accumulators are the P^T B operands as they stand. Lane (c, h) of S^T holds
-//   keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key group, so V is stored transposed with
-//   the keys of each 16-key group permuted to that order: the V^T A operand of an MFMA is
-//   one 16-byte LDS read.
-// - LDS rows are XOR-swizzled in 16-byte chunks: K by key & 7 (an A-operand read of 32
-//   keys spreads over all banks), V^T row d by (d ^ d >> 3) & 7 (the same for the V^T
-//   reads; the transposing writes, 4 bytes = 2 keys per lane, land at most 4 to a bank).
+//   keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key group: two runs of 4 consecutive keys,
+//   which is what one gfx950 transposing LDS read (ds_read_b64_tr_b16) returns from a
+//   row-major V. So V is stored like K, and each V^T A operand is two such reads (the
+//   earlier layout, V stored transposed with 4-byte writes of key pairs, spent more LDS
+//   cycles on the writes than on all other LDS work together).
+// - LDS rows (K and V) are XOR-swizzled in 16-byte chunks by key & 7, so a read of 32
+//   keys at one column spreads over all banks.
 // - When the head count is a multiple of 8, each XCD (workgroup ids are dealt round-robin
 //   over the 8 XCDs) gets a contiguous range of heads, i.e. few KV heads, so its L2 holds
 //   the K/V its workgroups re-read.
@@ -73,12 +74,6 @@ struct PrefillArgs {
 };
 
 __device__ __forceinline__ int kswz(int key) { return key & 7; }
-__device__ __forceinline__ int vswz(int d) { return (d ^ (d >> 3)) & 7; }
-// Position of key k (within its 16-key group) in a V^T row: lane half h reads keys
-// {4h..4h+3, 8+4h..8+4h+3} as 8 consecutive halves at 8h.
-__device__ __forceinline__ int vperm(int k) {
-  return (k & ~15) | (((k >> 2) & 1) << 3) | (((k >> 3) & 1) << 2) | (k & 3);
-}
 
 template <int D, bool POW2>
 __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillArgs a) {
@@ -94,10 +89,11 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
   constexpr int XSTRIP = DT * 16 * 64 + 2 * 64;             // floats per strip for the merge
   constexpr int SMEM = std::max(2 * KBUF + 2 * VBUF, 2 * 4 * XSTRIP);
 
-  // Two K and two V^T buffers; reused for the merge of the half-tile partials.
+  // Two K and two V buffers (row-major, 16-byte chunks XOR-swizzled by key); reused for the
+  // merge of the half-tile partials.
   __shared__ __attribute__((aligned(16))) half_t smem[SMEM];
   half_t* const sK = smem;
-  half_t* const sVt = smem + 2 * KBUF;
+  half_t* const sV = smem + 2 * KBUF;
 
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31, hh = lane >> 5;
@@ -174,16 +170,10 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
           half_t* kb = sK + buf * KBUF;
           *reinterpret_cast<half8*>(kb + kl * D + ((cc ^ kswz(kl)) << 3)) = kreg[2 * j];
           *reinterpret_cast<half8*>(kb + (kl + 1) * D + ((cc ^ kswz(kl + 1)) << 3)) = kreg[2 * j + 1];
-          // V^T: keys kl and kl+1 are adjacent in a V^T row (vperm keeps k & 3 in place),
-          // so each of the chunk's 8 dims is one 4-byte write.
-          const int pos = vperm(kl);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int d = 8 * cc + e;
-            const half2_t v2 = {vreg[2 * j][e], vreg[2 * j + 1][e]};
-            *reinterpret_cast<half2_t*>(sVt + buf * VBUF + d * kKeyTile + (((pos >> 3) ^ vswz(d)) << 3) + (pos & 7)) =
-                v2;
-          }
+          // V row-major like K (the PV operands come out of LDS through transposing reads).
+          half_t* vb = sV + buf * VBUF;
+          *reinterpret_cast<half8*>(vb + kl * D + ((cc ^ kswz(kl)) << 3)) = vreg[2 * j];
+          *reinterpret_cast<half8*>(vb + (kl + 1) * D + ((cc ^ kswz(kl + 1)) << 3)) = vreg[2 * j + 1];
         }
       }
     };
@@ -265,13 +255,21 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
           for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
       }
       m_run = m_new;
+      // V^T operand of lane (d, hh) for pb[u]: slots e < 4 hold keys kr .. kr + 3 and slots
+      // e >= 4 keys kr + 8 .. kr + 11 (the S^T accumulator order), kr = 32 (u / 2) + 16 (u % 2)
+      // + 4 hh; each run of 4 keys is one transposing read in which lane i16 of the 16-lane
+      // group reads row kr + i16 / 4, columns d0 + 4 (i16 % 4) .. +3.
+      const int i16 = lane & 15;
 #pragma unroll
       for (int u = 0; u < 2 * kSub; ++u)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int d = 32 * dt + c;
-          const half8 va = *reinterpret_cast<const half8*>(sVt + buf * VBUF + d * kKeyTile +
-                                                           (((4 * kSub * half + 2 * u + hh) ^ vswz(d)) << 3));
+          const int col = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (i16 & 3);
+          const int kr = 32 * kSub * half + 32 * (u >> 1) + 16 * (u & 1) + 4 * hh + (i16 >> 2);
+          const half_t* vb = sV + buf * VBUF + ((((col >> 3) ^ kswz(kr))) << 3) + (col & 7);
+          const half4 lo = tr_read_b64(vb + kr * D);
+          const half4 hi = tr_read_b64(vb + (kr + 8) * D);  // kswz(kr + 8) == kswz(kr)
+          const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[dt] = mfma32x32x16(va, pb[u], o[dt]);
         }
     };
