@@ -178,7 +178,7 @@ __device__ __forceinline__ int rope_tile_row(int tile, int m, int D) {
 // (m < 8) is row m + 8, held by lane (c, g + 2). The same float operations as qkv_post
 // (bias add, then a cs - b sn / b cs + a sn, products rounded, sincosf of pos * inv_freq[i]).
 __device__ __forceinline__ void rope_epilogue(const RopeArgs& ra, const float (&s)[4], int tile, int g, int t,
-                                              bool live, float* qkv, int N) {
+                                              bool live, float* qkv, int N, int p, int64_t kv_base) {
   const int D = ra.D, tph = D / 16, h = tile / tph, j0 = (tile - h * tph) * 8;
   const bool first = g < 2;
   float v[4];
@@ -191,13 +191,7 @@ __device__ __forceinline__ void rope_epilogue(const RopeArgs& ra, const float (&
 #pragma unroll
   for (int r = 0; r < 4; ++r) o[r] = __shfl_xor(v[r], 32);  // every lane takes part
   if (!live) return;
-  const int p = ra.pos[t];
   const bool rotate = h < ra.heads + ra.kv_heads;
-  int64_t kv_base = 0;
-  if (h >= ra.heads) {
-    const int block = ra.tables[ra.table_off[ra.seq[t]] + p / ra.block_size];
-    kv_base = kv_row_offset(block, ra.kv_heads, (h - ra.heads) % ra.kv_heads, ra.block_size, p % ra.block_size, D);
-  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * g + r, j = m < 8 ? j0 + m : D / 2 + j0 + m - 8;
@@ -231,6 +225,10 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   // (after a barrier; the launcher sizes that area for both).
   __shared__ float red_static[PRO == kPlain ? WAVES * NB * kWave * 4 : 1];
   __shared__ float s_inv[2 * kMaxTokens];
+  // kRope: each token's position and (k/v tiles) paged-cache row, looked up by the last wave
+  // while the others run the product (a chain of three dependent loads).
+  __shared__ int s_pos[EPI == kRope ? 2 * kMaxTokens : 1];
+  __shared__ int64_t s_kvrow[EPI == kRope ? 2 * kMaxTokens : 1];
   extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
   float* red = PRO == kPlain ? red_static : reinterpret_cast<float*>(sxb);
   const half_t* x = static_cast<const half_t*>(xin);
@@ -289,6 +287,19 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     __syncthreads();
   }
 
+  if (EPI == kRope && w == WAVES - 1) {
+    const int tph = ra.D / 16, h = blockIdx.x / tph;
+    for (int t = lane; t < T; t += kWave) {
+      const int p = ra.pos[t];
+      s_pos[t] = p;
+      if (h >= ra.heads) {
+        const int block = ra.tables[ra.table_off[ra.seq[t]] + p / ra.block_size];
+        s_kvrow[t] = kv_row_offset(block, ra.kv_heads, (h - ra.heads) % ra.kv_heads, ra.block_size,
+                                   p % ra.block_size, ra.D);
+      }
+    }
+  }
+
   float4v acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -336,7 +347,8 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[r] += red[((ww * NB + b) * kWave + lane) * 4 + r];
     if (EPI == kRope) {
-      rope_epilogue(ra, s, blockIdx.x, g, 16 * b + c, tok[b], y, N);
+      const int t = tok[b] ? 16 * b + c : 0;
+      rope_epilogue(ra, s, blockIdx.x, g, 16 * b + c, tok[b], y, N, s_pos[t], s_kvrow[t]);
       continue;
     }
     if (!tok[b]) continue;
