@@ -225,6 +225,39 @@ def bench_tinyllama_decode(steps, int8=False, n_seq=32, ctx=2048):
     return {"ms_wall": round(wall, 3), "ms_device": round(dev_ms, 3), "tok_s": round(n_seq / wall * 1e3, 1)}
 
 
+def bench_tinyllama_prefill(steps, S=2048):
+    """Config 3(a) as a whole forward pass: one S-token prompt in one chunk through all 22
+    layers (attention + rocBLAS GEMMs + layer kernels), synthetic fp16 weights; the dense
+    GEMM FLOPs 2 S (params) are reported next to the attention FLOPs."""
+    from relay_amd import HipBackend, HipOptions, tinyllama_1b
+    from relay_amd.backend import ForwardBatch, SeqChunk
+
+    c = tinyllama_1b()
+    bs = 16
+    nb = S // bs + 1
+    be = HipBackend(None, nb, bs, max_batch_tokens=S, max_context=nb * bs,
+                    options=HipOptions(False, False), config=c, synthetic_seed=0, synthetic_std=0.02)
+    rng = np.random.default_rng(0)
+    times = []
+    for r in range(steps + 2):
+        batch = ForwardBatch([SeqChunk(rng.integers(0, c.vocab, size=S).tolist(), 0, list(range(nb)), True)])
+        t0 = time.perf_counter()
+        be.forward(batch)
+        wall = (time.perf_counter() - t0) * 1e3
+        if r >= 2:
+            times.append((wall, be.last_forward_ms()))
+    be.close()
+    wall = float(np.median([t[0] for t in times]))
+    dev_ms = float(np.median([t[1] for t in times]))
+    params = c.layers * (c.hidden * (c.q_dim + 2 * c.kv_dim) + c.q_dim * c.hidden +
+                         3 * c.hidden * c.intermediate) + c.hidden * c.vocab
+    gemm_flops = 2.0 * S * (params - c.hidden * c.vocab) + 2.0 * c.hidden * c.vocab  # lm_head: last row only
+    attn_flops = 4.0 * c.head_dim * c.heads * S * (S + 1) / 2 * c.layers
+    return {"ms_wall": round(wall, 3), "ms_device": round(dev_ms, 3), "prompt_tok_s": round(S / wall * 1e3, 1),
+            "dense_gemm_tflop": round(gemm_flops / 1e12, 2), "attention_tflop": round(attn_flops / 1e12, 3),
+            "tflops_device": round((gemm_flops + attn_flops) / dev_ms / 1e9, 1)}
+
+
 # ---- config 1: SmolLM2-135M, 512-token prompt + 128 greedy steps --------------------------
 
 def bench_config1(prompt_len=512, new_tokens=128):
@@ -356,7 +389,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
-                                           "llama3decint8", "tinyllama"],
+                                           "llama3decint8", "tinyllama", "tinyllamaprefill"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
@@ -394,6 +427,8 @@ def main():
             r = bench_config1()
         elif args.leg == "tinyllama":
             r = bench_tinyllama_decode(args.steps)
+        elif args.leg == "tinyllamaprefill":
+            r = bench_tinyllama_prefill(args.steps)
         elif args.leg.startswith("llama3"):
             r = bench_llama3_mixed(args.steps, int8=args.leg.endswith("int8"),
                                    chunk=0 if args.leg.startswith("llama3dec") else 512)
@@ -416,6 +451,9 @@ def main():
         extra["tinyllama_decode_32x2048"] = td
         td8 = bench_tinyllama_decode(10, int8=True)
         extra["tinyllama_decode_32x2048_int8"] = td8
+        tp = bench_tinyllama_prefill(5)
+        log(f"tinyllama 2048-token prefill forward: {tp}")
+        extra["tinyllama_prefill_2048"] = tp
         c1 = bench_config1()
         log(f"config 1 (SmolLM2 512 + 128 greedy): {c1}")
         extra["smollm2_512_plus_128_greedy"] = c1
