@@ -397,7 +397,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's hot path (decode/prefill attention, int8 GEMV) runs on one "
-              "MI355X; multi-GPU sharding is described in DESIGN.md and not measured", file=sys.stderr)
+              "MI355X; the path is not sharded across GPUs in this build", file=sys.stderr)
         sys.exit(2)
     import torch
 
