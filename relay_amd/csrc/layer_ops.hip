@@ -215,6 +215,29 @@ __global__ void dequant_int8_kernel(const int8_t* w8, int64_t ldw, const float* 
   }
 }
 
+// 16 weights per thread: one 16-byte load of a row, two 16-byte stores (K % 16 == 0,
+// ldw % 16 == 0, aligned pointers); same per-element expression as dequant_int8_kernel.
+__global__ void dequant_int8_vec_kernel(const int8_t* w8, int64_t ldw, const float* scale, int K, int64_t pieces,
+                                        half_t* out) {
+  const int kp = K / 16;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < pieces;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t n = i / kp;
+    const int k = static_cast<int>(i - n * kp) * 16;
+    const uint4v q = *reinterpret_cast<const uint4v*>(w8 + n * ldw + k);
+    const float sc = scale[n];
+    half8 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo[e] = f16_of_product(static_cast<float>(static_cast<int8_t>(q[e / 4] >> (8 * (e % 4)))), sc);
+      hi[e] = f16_of_product(static_cast<float>(static_cast<int8_t>(q[2 + e / 4] >> (8 * (e % 4)))), sc);
+    }
+    half8* o = reinterpret_cast<half8*>(out + n * K + k);
+    o[0] = lo;
+    o[1] = hi;
+  }
+}
+
 // splitmix64 finalizer (Vigna), the mixing function of the synthetic-input generator.
 __device__ __host__ inline uint64_t mix64(uint64_t z) {
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -387,6 +410,14 @@ int rh_quantize_int8(const float* w, int N, int K, int8_t* q, int64_t ldq, float
 int rh_dequant_int8(const int8_t* w8, int64_t ldw, const float* scale, int N, int K, void* w16, void* stream) {
   RH_REQUIRE(N > 0 && K > 0 && ldw >= K, "dequant_int8: bad shape");
   const int64_t total = static_cast<int64_t>(N) * K;
+  if (K % 16 == 0 && ldw % 16 == 0 &&
+      (reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(w16)) % 16 == 0) {
+    const int64_t pieces = total / 16;
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(dequant_int8_vec_kernel, dim3(grid_for(pieces)), dim3(kThreads), 0,
+                                     static_cast<hipStream_t>(stream), w8, ldw, scale, K, pieces,
+                                     static_cast<half_t*>(w16)));
+    return 0;
+  }
   RH_TRY_LAUNCH(hipLaunchKernelGGL(dequant_int8_kernel, dim3(grid_for(total)), dim3(kThreads), 0,
                                    static_cast<hipStream_t>(stream), w8, ldw, scale, K, total,
                                    static_cast<half_t*>(w16)));

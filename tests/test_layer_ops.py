@@ -71,6 +71,24 @@ def test_quantize_int8_bit_exact(torch_mod, dev):
     assert np.array_equal(D.cpu().numpy().view(np.uint16), want.view(np.uint16))
 
 
+@pytest.mark.parametrize("N,K,ldq", [(300, 4096, 4096 + 256), (64, 14336, 14336 + 256), (33, 48, 64), (5, 40, 40)])
+def test_dequant_int8_bit_exact(torch_mod, dev, N, K, ldq):
+    """fp16(fp32(q * scale)) for every element, from padded rows (K % 16 == 0: 16 weights per
+    thread; otherwise one per thread)."""
+    from relay_amd import _lib
+
+    rng = np.random.default_rng(K + N)
+    q = rng.integers(-127, 128, size=(N, ldq)).astype(np.int8)
+    s = (rng.uniform(1e-4, 1e-2, N)).astype(np.float32)
+    Q, S = torch_mod.from_numpy(q).to(dev), torch_mod.from_numpy(s).to(dev)
+    D = torch_mod.empty((N, K), dtype=torch_mod.float16, device=dev)
+    print(f"dequant: N={N} K={K} ldq={ldq}", flush=True)
+    _lib.check(_lib.lib().rh_dequant_int8(Q.data_ptr(), ldq, S.data_ptr(), N, K, D.data_ptr(), None), "rh_dequant_int8")
+    torch_mod.cuda.synchronize()
+    want = (q[:, :K].astype(np.float32) * s[:, None]).astype(np.float16)
+    assert np.array_equal(D.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
 def test_kv_gather_scatter_round_trip(torch_mod, dev):
     from relay_amd import _lib
 
