@@ -21,11 +21,12 @@
 // One barrier per step: step s reads buffer s & 1 and fills buffer (s + 1) & 1, which every
 // wave finished reading before the previous barrier.
 //
-// Measured on MI355X at Llama-3-8B shapes, T = 560: 430-470 TFLOP/s where the grid has
-// >= 1000 workgroups (N = 28672), 280-400 on the 32-48-tile grids of N = 4096-6144 (dequantize
-// + library GEMM is faster there, and the backend uses it); 128x128 tiles, 128-k steps and
-// prefetching 2-4 steps ahead through more register sets were all slower (the registers cut
-// occupancy). The template keeps the tile shape and prefetch depth as parameters.
+// Measured on MI355X at Llama-3-8B shapes: 430-470 TFLOP/s where the grid has >= 1000
+// workgroups (N = 28672, T = 560), 280-400 on the 32-48-tile grids of N = 4096-6144; it wins
+// while the weights dominate (T up to a few hundred), and dequantize + library GEMM wins
+// once the product is compute-bound. 128x128 tiles, 128-k steps and prefetching 2-4 steps
+// ahead through more register sets were all slower (the registers cut occupancy). The
+// template keeps the tile shape and prefetch depth as parameters.
 #include "../../include/relay_hip.h"
 #include "common.h"
 

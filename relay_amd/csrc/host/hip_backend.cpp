@@ -353,14 +353,15 @@ bool HipBackend::fused(const DeviceMatrix& W, int T) const {
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
   // int8 (measured at Llama-3-8B shapes): the GEMV up to 16 tokens; the int8 GEMM for wide
-  // matrices (N >= 16384: a grid of >= 1000 workgroups at T = 560, 1.1-3.5x faster than
-  // dequantize + GEMM); the GEMV up to 64 tokens on narrower ones; otherwise dequantize +
-  // library GEMM (relay's path for every T above its GEMV limit).
-  if (T <= 16 || (T <= rh_gemv_int8_max_tokens() && !(W.N >= 16384 && W.K % 64 == 0))) {
+  // matrices (N >= 16384) up to 256 tokens (3.5x faster than dequantize + GEMM at T = 48);
+  // the GEMV up to 64 tokens on narrower ones; otherwise dequantize + library GEMM (relay's
+  // path for every T above its GEMV limit), which wins once the GEMM is compute-bound.
+  const bool wide = W.N >= 16384 && W.K % 64 == 0 && T <= 256;
+  if (T <= 16 || (T <= rh_gemv_int8_max_tokens() && !wide)) {
     RH_CHECK(rh_gemv_int8(W.i8.p, W.ldw, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
     return;
   }
-  if (W.N >= 16384 && W.K % 64 == 0) {
+  if (wide) {
     RH_CHECK(rh_gemm_w8(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, stream_));
     return;
   }
