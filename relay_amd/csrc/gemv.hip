@@ -58,23 +58,27 @@ __device__ __forceinline__ half8 int8x8_to_half8(uint32_t lo, uint32_t hi) {
   return v - bias;
 }
 
-// T <= 16 * NB tokens: NB column blocks of 16 tokens share each converted A operand. Fewer
-// chunks per load batch as NB grows keeps the activation operands in registers.
-template <int WAVES, int NB, bool F16_SCALE>
+// T <= 16 * NB tokens: NB column blocks of 16 tokens share each converted A operand, and
+// RT 16-row tiles share each activation operand (a workgroup covers 16 RT rows: above 16
+// tokens every workgroup re-reads all T activation rows of K through L2, so fewer, taller
+// workgroups read less). Fewer chunks per load batch as NB grows keeps the operands in
+// registers.
+template <int WAVES, int NB, int RT, bool F16_SCALE>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                   const void* __restrict__ scale,
                                                                   const half_t* __restrict__ x, float* y, int T,
                                                                   int K, int N, float beta) {
   constexpr int U = NB == 1 ? kUnroll : (NB == 2 ? 2 : 1);
-  __shared__ float red[WAVES][NB][kWave * 4];
+  __shared__ float red[WAVES][RT][NB][kWave * 4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int row = min(n0 + c, N - 1);
+  const int n0 = blockIdx.x * 16 * RT;
   const int nchunks = (K + kChunk - 1) / kChunk;
   const int per = (nchunks + WAVES - 1) / WAVES;
   const int cb = w * per, ce = min(nchunks, cb + per);
-  const int8_t* wrow = w8 + static_cast<int64_t>(row) * ldw;
+  const int8_t* wrow[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wrow[rt] = w8 + static_cast<int64_t>(min(n0 + 16 * rt + c, N - 1)) * ldw;
   bool tok[NB];
   const half_t* xrow[NB];
 #pragma unroll
@@ -84,17 +88,21 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   }
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 
-  float4v acc[NB];
+  float4v acc[RT][NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[rt][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   for (int q0 = cb; q0 < ce; q0 += U) {
-    uint4v wv[U];
+    uint4v wv[RT][U];
     half8 xa[NB][U], xb[NB][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (q0 + u) * kChunk + 16 * g;
       const bool live = q0 + u < ce && k < K;
-      wv[u] = live ? *reinterpret_cast<const uint4v*>(wrow + k) : uint4v{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        wv[rt][u] = live ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
@@ -102,42 +110,48 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const half8 a0 = int8x8_to_half8(wv[u][0], wv[u][1]);
-      const half8 a1 = int8x8_to_half8(wv[u][2], wv[u][3]);
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        acc[b] = mfma16x16x32(a0, xa[b][u], acc[b]);
-        acc[b] = mfma16x16x32(a1, xb[b][u], acc[b]);
+      for (int rt = 0; rt < RT; ++rt) {
+        const half8 a0 = int8x8_to_half8(wv[rt][u][0], wv[rt][u][1]);
+        const half8 a1 = int8x8_to_half8(wv[rt][u][2], wv[rt][u][3]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          acc[rt][b] = mfma16x16x32(a0, xa[b][u], acc[rt][b]);
+          acc[rt][b] = mfma16x16x32(a1, xb[b][u], acc[rt][b]);
+        }
       }
-    }
   }
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[w][b][lane * 4 + r] = acc[b][r];
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[w][rt][b][lane * 4 + r] = acc[rt][b][r];
   __syncthreads();
   if (w != 0) return;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    // Lane (c, g) now sums the waves for token 16b + c, rows n0 + 4g + r, in a fixed order.
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww)
+    for (int b = 0; b < NB; ++b) {
+      // Lane (c, g) sums the waves for token 16b + c, rows n0 + 16 rt + 4g + r, in a fixed order.
+      float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] += red[ww][b][lane * 4 + r];
-    if (!tok[b]) continue;
+      for (int ww = 0; ww < WAVES; ++ww)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = n0 + 4 * g + r;
-      if (n >= N) continue;
-      float sc;
-      if (F16_SCALE) sc = static_cast<float>(static_cast<const half_t*>(scale)[n]);
-      else sc = static_cast<const float*>(scale)[n];
-      float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
-      *dst = s[r] * sc + (beta != 0.0f ? beta * *dst : 0.0f);
+        for (int r = 0; r < 4; ++r) s[r] += red[ww][rt][b][lane * 4 + r];
+      if (!tok[b]) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 16 * rt + 4 * g + r;
+        if (n >= N) continue;
+        float sc;
+        if (F16_SCALE) sc = static_cast<float>(static_cast<const half_t*>(scale)[n]);
+        else sc = static_cast<const float*>(scale)[n];
+        float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+        *dst = s[r] * sc + (beta != 0.0f ? beta * *dst : 0.0f);
+      }
     }
-  }
 }
 
 // What the fp16 kernel's B operands are made from:
@@ -362,16 +376,16 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
 }
 
-template <int NB, bool F16_SCALE>
+template <int NB, int RT, bool F16_SCALE>
 int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
               float beta, hipStream_t s) {
-  const int tiles = (N + 15) / 16;
+  const int tiles = (N + 16 * RT - 1) / (16 * RT);
   if (tiles < 256) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, NB, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s,
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, NB, RT, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s,
                                      w8, ldw, scale, x, y, T, K, N, beta));
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, NB, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s, w8,
-                                     ldw, scale, x, y, T, K, N, beta));
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, NB, RT, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s,
+                                     w8, ldw, scale, x, y, T, K, N, beta));
   }
   return 0;
 }
@@ -379,10 +393,16 @@ int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x,
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
-  if (T <= 16) return launch_nb<1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
-  if (T <= 32) return launch_nb<2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
-  if (T <= 48) return launch_nb<3, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
-  return launch_nb<4, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  if (T <= 16) return launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  // Two row tiles per workgroup only while that still leaves >= 192 workgroups (measured at
+  // T = 17-64: N = 6144 gains up to 30%, N = 4096 with 128 workgroups loses as much).
+  const bool tall = (N + 31) / 32 >= 192;
+  if (T <= 32) return tall ? launch_nb<2, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
+                           : launch_nb<2, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  if (T <= 48) return tall ? launch_nb<3, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
+                           : launch_nb<3, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  return tall ? launch_nb<4, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
+              : launch_nb<4, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
 }
 
 }  // namespace

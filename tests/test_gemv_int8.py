@@ -56,7 +56,7 @@ def bound(w8, scale, x_bits):
 
 
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 7, 8, 9, 16, 17, 32, 33, 48, 64])
-@pytest.mark.parametrize("N,K", [(64, 4096), (1000, 1024), (48, 80), (33, 160), (4096, 576)])
+@pytest.mark.parametrize("N,K", [(64, 4096), (1000, 1024), (48, 80), (33, 160), (4096, 576), (6150, 256)])
 def test_matches_oracle(torch_mod, dev, T, N, K):
     w8, s, x = make(N, K, T, seed=T * 1000 + N + K)
     y = run(torch_mod, dev, w8, s, x)
