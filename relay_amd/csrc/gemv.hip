@@ -1,4 +1,4 @@
-// Skinny products for decode batches on gfx950: weight-only int8 (T <= 16 tokens) and fp16
+// Skinny products for decode batches on gfx950: weight-only int8 (T <= 64 tokens) and fp16
 // weights (T <= 32 tokens).
 //
 //   y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n])       rh_gemv_int8
