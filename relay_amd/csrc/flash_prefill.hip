@@ -29,8 +29,8 @@
 //   row-major V. So V is stored like K, and each V^T A operand is two such reads (the
 //   earlier layout, V stored transposed with 4-byte writes of key pairs, spent more LDS
 //   cycles on the writes than on all other LDS work together).
-// - LDS rows (K and V) are XOR-swizzled in 16-byte chunks by key & 7, so a read of 32
-//   keys at one column spreads over all banks.
+// - LDS rows (K and V) are XOR-swizzled in 16-byte chunks by key (kswz), so a read of 32
+//   keys at one column spreads over the banks.
 // - When the head count is a multiple of 8, each XCD (workgroup ids are dealt round-robin
 //   over the 8 XCDs) gets a contiguous range of heads, i.e. few KV heads, so its L2 holds
 //   the K/V its workgroups re-read.
@@ -73,7 +73,11 @@ struct PrefillArgs {
   int64_t out_stride;
 };
 
-__device__ __forceinline__ int kswz(int key) { return key & 7; }
+// 16-byte chunk swizzle of K and V rows by key. At D128 keys 8 apart also get different
+// chunks (bank conflicts halved, 56.3 -> 55.0 us at 2048 tokens); at D64 the same change
+// measured slower (32.4 -> 34.0 us), so it keeps key & 7.
+template <int D>
+__device__ __forceinline__ int kswz(int key) { return D == 128 ? (key ^ ((key >> 3) & 3)) & 7 : key & 7; }
 
 template <int D, bool POW2>
 __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillArgs a) {
@@ -168,12 +172,12 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
         int kl, cc;
         if (item(2 * j, kl, cc)) {
           half_t* kb = sK + buf * KBUF;
-          *reinterpret_cast<half8*>(kb + kl * D + ((cc ^ kswz(kl)) << 3)) = kreg[2 * j];
-          *reinterpret_cast<half8*>(kb + (kl + 1) * D + ((cc ^ kswz(kl + 1)) << 3)) = kreg[2 * j + 1];
+          *reinterpret_cast<half8*>(kb + kl * D + ((cc ^ kswz<D>(kl)) << 3)) = kreg[2 * j];
+          *reinterpret_cast<half8*>(kb + (kl + 1) * D + ((cc ^ kswz<D>(kl + 1)) << 3)) = kreg[2 * j + 1];
           // V row-major like K (the PV operands come out of LDS through transposing reads).
           half_t* vb = sV + buf * VBUF;
-          *reinterpret_cast<half8*>(vb + kl * D + ((cc ^ kswz(kl)) << 3)) = vreg[2 * j];
-          *reinterpret_cast<half8*>(vb + (kl + 1) * D + ((cc ^ kswz(kl + 1)) << 3)) = vreg[2 * j + 1];
+          *reinterpret_cast<half8*>(vb + kl * D + ((cc ^ kswz<D>(kl)) << 3)) = vreg[2 * j];
+          *reinterpret_cast<half8*>(vb + (kl + 1) * D + ((cc ^ kswz<D>(kl + 1)) << 3)) = vreg[2 * j + 1];
         }
       }
     };
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
 #pragma unroll
         for (int j = 0; j < kSub; ++j) {
           const half_t* kt = sK + buf * KBUF + (32 * kSub * half + 32 * j + c) * D;
-          const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz(c)) << 3));
+          const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz<D>(c)) << 3));
           s[j] = mfma32x32x16(ka, qb[m], s[j]);
         }
       float mx = -INFINITY;
@@ -266,9 +270,9 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
         for (int dt = 0; dt < DT; ++dt) {
           const int col = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (i16 & 3);
           const int kr = 32 * kSub * half + 32 * (u >> 1) + 16 * (u & 1) + 4 * hh + (i16 >> 2);
-          const half_t* vb = sV + buf * VBUF + ((((col >> 3) ^ kswz(kr))) << 3) + (col & 7);
-          const half4 lo = tr_read_b64(vb + kr * D);
-          const half4 hi = tr_read_b64(vb + (kr + 8) * D);  // kswz(kr + 8) == kswz(kr)
+          const half_t* vb = sV + buf * VBUF + (col & 7);
+          const half4 lo = tr_read_b64(vb + kr * D + (((col >> 3) ^ kswz<D>(kr)) << 3));
+          const half4 hi = tr_read_b64(vb + (kr + 8) * D + (((col >> 3) ^ kswz<D>(kr + 8)) << 3));
           const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[dt] = mfma32x32x16(va, pb[u], o[dt]);
         }
