@@ -77,3 +77,15 @@ def test_prefill_8192_tokens_against_fp32_torch(torch_mod, dev):
     got = run_prefill(torch_mod, dev, case)
     want = _torch_causal_attention(torch_mod, dev, case)
     check_close(got, want)
+
+
+def test_decode_64k_context(torch_mod, dev):
+    """One sequence at 65536 keys (D 128, 32 q / 8 kv heads): the planner splits it into
+    more slices than one batched merge takes, so the general merge loop runs."""
+    from relay_amd import _lib
+
+    case = PagedCase([65536], 1, 32, 8, 128, 16, seed=64)
+    slice_keys = _lib.lib().rh_decode_slice_keys(1, 8, 4, 128, 65536)
+    assert math.ceil(65536 / slice_keys) > 8
+    got, _ = run_decode(torch_mod, dev, case)
+    check_close(got, oracle_out(case))
