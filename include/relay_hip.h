@@ -149,6 +149,19 @@ int rh_gemv_int8_max_tokens(void);
 int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
                 void* stream);
 
+/* rh_gemv_f16 with K cut into ksplit ranges (1 <= ksplit <= 8, at most one per 64 values of
+ * K), each its own workgroup, so that small-N products still cover the GPU. Partial sums go
+ * to workspace (fp32, ksplit * T * N values) and the last workgroup of each 16-row tile to
+ * finish adds them in range order (deterministic); counters holds ceil(N / 16) ints that
+ * must be zero before the first call (each call leaves them zero). Calls that share a
+ * workspace or counters must not overlap. ksplit = 1 is rh_gemv_f16 (workspace and
+ * counters unused). No counterpart in relay (cublasGemmEx, cuda_backend.cu:726-730). */
+int rh_gemv_f16_splitk(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N, float beta,
+                       int ksplit, float* workspace, int* counters, void* stream);
+
+/* The ksplit rh_gemv_f16_splitk is fastest with for this shape (measured on MI355X). */
+int rh_gemv_f16_split_plan(int T, int K, int N);
+
 /* rh_gemv_f16 with the producer of x folded in (no counterpart in relay, where
  * rms_norm_kernel / silu_mul_kernel run as their own launches before the GEMM,
  * cuda_backend.cu:576-591). Each workgroup computes x for all T tokens into LDS:
@@ -171,6 +184,14 @@ int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const 
                             float* qkv, int T, int K, const float* bias, const float* inv_freq, const int* pos,
                             const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
                             void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream);
+
+/* The same with x already fp16 [T, K] (no normalisation): rh_gemv_f16 then rh_qkv_post in
+ * one launch, for the token counts where the RMSNorm cannot be folded in (1 <= T <= 32).
+ * No counterpart in relay (cuda_backend.cu:577-578 are two launches). */
+int rh_gemv_f16_qkv(const void* w16, int64_t ldw, const void* x, float* qkv, int T, int K, const float* bias,
+                    const float* inv_freq, const int* pos, const int* seq, const int* table_off, const int* tables,
+                    void* kpool, void* vpool, void* q_out, int heads, int kv_heads, int head_dim, int block_size,
+                    void* stream);
 
 /* Largest T rh_gemv_f16 takes. */
 int rh_gemv_f16_max_tokens(void);

@@ -58,12 +58,15 @@ SIGNATURES = {
     "rh_gemv_int8": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
     "rh_gemv_int8_row_stride": (I64, [I]),
     "rh_gemv_f16": (I, [P, I64, P, P, I, I, I, F, P]),
+    "rh_gemv_f16_splitk": (I, [P, I64, P, P, I, I, I, F, I, P, P, P]),
+    "rh_gemv_f16_split_plan": (I, [I, I, I]),
     "rh_gemv_f16_max_tokens": (I, []),
     "rh_gemm_w8": (I, [P, I64, P, P, P, I, I, I, F, P]),
     "rh_gemv_f16_rmsnorm": (I, [P, I64, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_f16_silu": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_fused_fits": (I, [I, I]),
     "rh_gemv_f16_rmsnorm_qkv": (I, [P, I64, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_gemv_f16_qkv": (I, [P, I64, P, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
     "rh_gemv_int8_max_tokens": (I, []),
     "rh_quantize_int8": (I, [P, I, I, P, I64, P, P]),
     "rh_dequant_int8": (I, [P, I64, P, I, I, P, P]),

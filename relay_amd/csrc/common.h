@@ -105,6 +105,16 @@ __device__ __forceinline__ int64_t kv_row_offset(int block, int kv_heads, int kv
   return ((static_cast<int64_t>(block) * kv_heads + kvh) * block_size + slot) * static_cast<int64_t>(D);
 }
 
+// Stores and loads that are coherent across the device's XCDs for this location (sc1
+// accesses): how partial results pass between workgroups (a slice or K-range merge by the
+// last workgroup to arrive, ordered by an agent-scope atomic counter).
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace relay_hip
 
 // ---- host-side error plumbing for the C ABI ------------------------------------------

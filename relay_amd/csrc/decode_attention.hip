@@ -62,15 +62,6 @@ struct DecodeArgs {
   int64_t out_stride;
 };
 
-// Stores and loads that are coherent across the device's XCDs for this location (sc1
-// accesses): what the slice merge shares between workgroups.
-__device__ __forceinline__ void coherent_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float coherent_load(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Slices merged with all their loads issued together (more take a plain loop).
 constexpr int kMergeBatch = 8;
 

@@ -88,9 +88,10 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   }
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 
-  // Wave 0 writes the results. Its row scales (and the old y for beta != 0) are loaded
-  // before the weights: issued after the reduction they would queue behind the weight
-  // stream (measured 0.7-3.8 us of dependent-load tail).
+  // Wave 0 writes the results. Its row scales (and the old y for beta != 0, where the
+  // registers allow) are loaded before the weights: issued after the reduction they would
+  // queue behind the weight stream (measured 0.7-3.8 us of dependent-load tail).
+  constexpr bool kEarlyY = NB * RT <= 2;
   float sc[RT][4], yold[RT][NB][4];
   if (w == 0) {
 #pragma unroll
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
         else sc[rt][r] = static_cast<const float*>(scale)[n];
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-          yold[rt][b][r] = beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + n] : 0.0f;
+          yold[rt][b][r] = kEarlyY && beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + n] : 0.0f;
       }
   }
 
@@ -163,7 +164,8 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
       for (int r = 0; r < 4; ++r) {
         const int n = n0 + 16 * rt + 4 * g + r;
         if (n >= N) continue;
-        y[static_cast<int64_t>(16 * b + c) * N + n] = s[r] * sc[rt][r] + (beta != 0.0f ? beta * yold[rt][b][r] : 0.0f);
+        float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+        *dst = s[r] * sc[rt][r] + (beta != 0.0f ? beta * (kEarlyY ? yold[rt][b][r] : *dst) : 0.0f);
       }
     }
 }
@@ -195,6 +197,14 @@ struct RopeArgs {
   half_t* vc;
   half_t* q_out;  // [T, heads * D] or null
   int heads, kv_heads, D, block_size;
+};
+
+// Split-K partials of the plain fp16 product: ws [ksn][T][N] fp32, one counter per 16-row
+// tile (zero between launches; the merging workgroup resets it).
+constexpr int kMaxSplit = 8;
+struct SplitArgs {
+  float* ws;
+  int* counters;
 };
 
 __device__ __forceinline__ int rope_tile_row(int tile, int m, int D) {
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
                                                                  const void* __restrict__ xin,
                                                                  const float* __restrict__ norm_w, float eps,
                                                                  float* y, int T, int K, int N, float beta,
-                                                                 RopeArgs ra) {
+                                                                 RopeArgs ra, SplitArgs sp) {
   // The cross-wave reduction buffer; with a prologue it reuses the staged activations' LDS
   // (after a barrier; the launcher sizes that area for both).
   __shared__ float red_static[PRO == kPlain ? WAVES * NB * kWave * 4 : 1];
@@ -273,9 +283,12 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   const int c = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int row = EPI == kRope ? rope_tile_row(blockIdx.x, c, ra.D) : min(n0 + c, N - 1);
+  // K range of this workgroup (blockIdx.y of gridDim.y), split among its waves.
   const int nchunks = (K + kChunk - 1) / kChunk;
-  const int per = (nchunks + WAVES - 1) / WAVES;
-  const int cb = w * per, ce = min(nchunks, cb + per);
+  const int ks = blockIdx.y, ksn = gridDim.y;
+  const int kc0 = ks * nchunks / ksn, kc1 = (ks + 1) * nchunks / ksn;
+  const int per = (kc1 - kc0 + WAVES - 1) / WAVES;
+  const int cb = kc0 + w * per, ce = min(kc1, cb + per);
   const half_t* wrow = wt + static_cast<int64_t>(row) * ldw;
   bool tok[NB];
   const half_t* xrow[NB];
@@ -298,15 +311,17 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     }
   };
   load_w(cb);
-  // Wave 0's old y (beta != 0) before the stream, not behind it.
+  // Wave 0's old y (beta != 0) or RoPE operands before the stream, not behind it (for one
+  // token block: more would spill in the 16-wave instances).
+  constexpr bool kEarlyY = NB == 1;
   float yold[NB][4], rbias[4], rfreq[4];
-  if (EPI == kRope && w == 0) rope_operands(ra, blockIdx.x, g, rbias, rfreq);
+  if (EPI == kRope && kEarlyY && w == 0) rope_operands(ra, blockIdx.x, g, rbias, rfreq);
   if (EPI == kStore && w == 0) {
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        yold[b][r] = beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + min(n0 + 4 * g + r, N - 1)] : 0.0f;
+        yold[b][r] = kEarlyY && beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + min(n0 + 4 * g + r, N - 1)] : 0.0f;
   }
   if (PRO == kRmsNorm) {
     const float* xf = static_cast<const float*>(xin);
@@ -385,25 +400,77 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
     for (int r = 0; r < 4; ++r) red[((w * NB + b) * kWave + lane) * 4 + r] = acc[b][r];
   __syncthreads();
   if (w != 0) return;
+  // Lane (c, g) sums the waves for token 16b + c, rows n0 + 4g + r, in a fixed order.
+  auto wave_sum = [&](int b, float (&v)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[r] = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww) v[r] += red[((ww * NB + b) * kWave + lane) * 4 + r];
+    }
+  };
+  if (EPI == kRope) {
+    if (!kEarlyY) rope_operands(ra, blockIdx.x, g, rbias, rfreq);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float v[4];
+      wave_sum(b, v);
+      const int t = tok[b] ? 16 * b + c : 0;
+      rope_epilogue(ra, v, rbias, rfreq, blockIdx.x, g, 16 * b + c, tok[b], y, N, s_pos[t], s_kvrow[t]);
+    }
+    return;
+  }
+  float sum[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) wave_sum(b, sum[b]);
+  if (ksn > 1) {
+    // Split K: publish this K range's sums; the last workgroup of the row tile to arrive
+    // adds the ksn partials in K-range order (the same sum whichever arrives last).
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 4 * g + r;
+        if (tok[b] && n < N) coherent_store(&sp.ws[(static_cast<int64_t>(ks) * T + 16 * b + c) * N + n], sum[b][r]);
+      }
+    __builtin_amdgcn_s_waitcnt(0);
+    int last = 0;
+    if (lane == 0) {
+      const int prev = __hip_atomic_fetch_add(&sp.counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == ksn - 1;
+      if (last) __hip_atomic_store(&sp.counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!__shfl(last, 0)) return;
+    // One token block at a time (all its partials' loads in flight together).
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float part[kMaxSplit][4];
+#pragma unroll
+      for (int q = 0; q < kMaxSplit; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = min(n0 + 4 * g + r, N - 1), t = tok[b] ? 16 * b + c : 0;
+          part[q][r] = q < ksn && q != ks ? coherent_load(&sp.ws[(static_cast<int64_t>(q) * T + t) * N + n]) : sum[b][r];
+        }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kMaxSplit; ++q)
+          if (q < ksn) v += part[q][r];
+        sum[b][r] = v;
+      }
+    }
+  }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    // Lane (c, g) sums the waves for token 16b + c, rows n0 + 4g + r, in a fixed order.
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] += red[((ww * NB + b) * kWave + lane) * 4 + r];
-    if (EPI == kRope) {
-      const int t = tok[b] ? 16 * b + c : 0;
-      rope_epilogue(ra, s, rbias, rfreq, blockIdx.x, g, 16 * b + c, tok[b], y, N, s_pos[t], s_kvrow[t]);
-      continue;
-    }
     if (!tok[b]) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int n = n0 + 4 * g + r;
       if (n >= N) continue;
-      y[static_cast<int64_t>(16 * b + c) * N + n] = s[r] + (beta != 0.0f ? beta * yold[b][r] : 0.0f);
+      float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+      *dst = sum[b][r] + (beta != 0.0f ? beta * (kEarlyY ? yold[b][r] : *dst) : 0.0f);
     }
   }
 }
@@ -467,7 +534,8 @@ extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
 
 template <int PRO, int EPI = kStore>
 static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const float* norm_w, float eps, float* y,
-                           int T, int K, int N, float beta, void* stream, const RopeArgs& ra = RopeArgs{}) {
+                           int T, int K, int N, float beta, void* stream, const RopeArgs& ra = RopeArgs{},
+                           int ksplit = 1, const SplitArgs& sp = SplitArgs{}) {
   RH_REQUIRE(T >= 1 && T <= 2 * kMaxTokens, "gemv_f16: T must be in 1..32");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_f16: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
@@ -478,11 +546,12 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* wt = static_cast<const half_t*>(w16);
   const int tiles = (N + 15) / 16;
-  const bool wide = tiles < 256;
+  // 16 waves while the grid is below one workgroup per CU and each has >= 16 chunks of K.
+  const bool wide = tiles * ksplit < 256 && (K + kChunk - 1) / kChunk / ksplit >= 16;
 #define RH_GEMV_F16(W, NBLK)                                                                                    \
-  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles), dim3(W * kWave),             \
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles, ksplit), dim3(W * kWave),     \
                                    PRO == kPlain ? 0 : std::max<size_t>(staged, W * NBLK * kWave * 4 * sizeof(float)), s, wt, \
-                                   ldw, x, norm_w, eps, y, T, K, N, beta, ra))
+                                   ldw, x, norm_w, eps, y, T, K, N, beta, ra, sp))
   if (T <= kMaxTokens) {
     if (wide) {
       RH_GEMV_F16(16, 1);
@@ -503,6 +572,25 @@ extern "C" int rh_gemv_f16(const void* w16, int64_t ldw, const void* x, float* y
   return gemv_f16_launch<kPlain>(w16, ldw, x, nullptr, 0.0f, y, T, K, N, beta, stream);
 }
 
+extern "C" int rh_gemv_f16_split_plan(int T, int K, int N) {
+  if (T < 1 || K <= 0 || N <= 0) return -1;
+  // Measured on MI355X (T = 1-32): the merge costs ~3 us (stores, counter, loads), so only
+  // a long K on few row tiles gains (N = 2048, K = 5632, T = 32: 18.5 -> 14.4 us); ranges of
+  // K on wider grids, or more than two, were slower everywhere.
+  const int tiles = (N + 15) / 16, nchunks = (K + kChunk - 1) / kChunk;
+  return tiles <= 128 && nchunks >= 64 ? 2 : 1;
+}
+
+extern "C" int rh_gemv_f16_splitk(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N,
+                                  float beta, int ksplit, float* workspace, int* counters, void* stream) {
+  RH_REQUIRE(ksplit >= 1 && ksplit <= kMaxSplit, "gemv_f16_splitk: ksplit must be in 1..8");
+  RH_REQUIRE(ksplit <= (K + kChunk - 1) / kChunk, "gemv_f16_splitk: more K ranges than 64-wide chunks of K");
+  RH_REQUIRE(ksplit == 1 || (workspace != nullptr && counters != nullptr),
+             "gemv_f16_splitk: ksplit > 1 needs a workspace and counters");
+  return gemv_f16_launch<kPlain>(w16, ldw, x, nullptr, 0.0f, y, T, K, N, beta, stream, RopeArgs{}, ksplit,
+                                 SplitArgs{workspace, counters});
+}
+
 extern "C" int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
                                    float* y, int T, int K, int N, float beta, void* stream) {
   RH_REQUIRE(norm_w != nullptr, "gemv_f16_rmsnorm: no norm weights");
@@ -512,6 +600,20 @@ extern "C" int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x,
 extern "C" int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N,
                                 float beta, void* stream) {
   return gemv_f16_launch<kSiluMul>(w16, ldw, gu, nullptr, 0.0f, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_f16_qkv(const void* w16, int64_t ldw, const void* x, float* qkv, int T, int K,
+                               const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                               const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out,
+                               int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+  RH_REQUIRE(inv_freq && pos && seq && table_off && tables && kpool && vpool, "gemv_f16_qkv: missing pointer");
+  RH_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gemv_f16_qkv: bad head counts");
+  RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "gemv_f16_qkv: head_dim must be a multiple of 16");
+  RH_REQUIRE(block_size > 0, "gemv_f16_qkv: bad block size");
+  RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
+              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  return gemv_f16_launch<kPlain, kRope>(w16, ldw, x, nullptr, 0.0f, qkv, T, K, N, 0.0f, stream, ra);
 }
 
 extern "C" int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,

@@ -181,6 +181,8 @@ class HipBackend final : public Backend {
   void gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta);
   bool fused(const DeviceMatrix& W, int T) const;
   void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
+  // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
+  static bool skinny(int K, int N, int T);
   void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
 
   ModelConfig c_;
@@ -210,6 +212,8 @@ class HipBackend final : public Backend {
   PinnedBuffer logits_host_;
   DeviceArray<float> part_o_, part_ml_;
   DeviceArray<int> counters_;
+  DeviceArray<float> split_ws_;      // K-range partials of the split skinny product
+  DeviceArray<int> split_counters_;  // its per-tile arrival counters (zero between calls)
 
   std::mutex copy_mu_;
   DeviceArray<unsigned char> kv_stage_dev_;
@@ -329,12 +333,23 @@ void HipBackend::load_weights(const WeightSource& src) {
 }
 
 void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta) {
-  // Decode batch sizes: the skinny MFMA kernel (the library GEMM spends ~8 us per call on
-  // small matrices). Measured crossover: the library is as fast from T = 16 to 24 up, and
-  // faster at T = 32 (TinyLlama 32 x 2048 decode step: 2.33 vs 2.53 ms; folding RMSNorm into
-  // the product at T = 32 costs 6.0 ms: every workgroup normalises all 32 rows).
-  if (T <= 16 && K % 16 == 0) {
-    RH_CHECK(rh_gemv_f16(W, K, x, y, T, K, N, beta, stream_));
+  // Decode batch sizes: the skinny MFMA product (the library GEMM spends ~8-12 us per call on
+  // small matrices). Up to 16 tokens for every matrix; at 17-32 tokens only up to N = 4096,
+  // where it is ahead (TinyLlama shapes at T = 32: qkv 2560 x 2048 8.8 vs 12.0 us, wo 8.7 vs
+  // 12.0, down 2048 x 5632 with K split in two 14.4 vs 16.2) and the library kernels win on
+  // the wider gate_up (21.6 vs 15.9 us) and lm_head.
+  if (skinny(K, N, T)) {
+    const int ks = rh_gemv_f16_split_plan(T, K, N);
+    if (ks > 1) {
+      const std::size_t need = static_cast<std::size_t>(ks) * T * N;
+      if (need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
+      const std::size_t tiles = (N + 15) / 16;
+      if (tiles > split_counters_.n) {
+        split_counters_ = DeviceArray<int>(tiles);
+        HIP_CHECK(hipMemsetAsync(split_counters_.p, 0, tiles * sizeof(int), stream_));
+      }
+    }
+    RH_CHECK(rh_gemv_f16_splitk(W, K, x, y, T, K, N, beta, ks, split_ws_.p, split_counters_.p, stream_));
     return;
   }
   // Row-major y[T, N] = x[T, K] W[N, K]^T is column-major y^T (N x T) = W^T-view (K x N)^T x^T.
@@ -343,6 +358,10 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
                                 rocblas_datatype_f16_r, K, x, rocblas_datatype_f16_r, K, &beta, y,
                                 rocblas_datatype_f32_r, N, y, rocblas_datatype_f32_r, N, rocblas_datatype_f32_r,
                                 rocblas_gemm_algo_standard, 0, 0));
+}
+
+bool HipBackend::skinny(int K, int N, int T) {
+  return K % 16 == 0 && (T <= 16 || (T <= rh_gemv_f16_max_tokens() && N <= 4096));
 }
 
 bool HipBackend::fused(const DeviceMatrix& W, int T) const {
@@ -483,6 +502,11 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
       RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
                                        d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
                                        layout_.block_size, stream_));
+    } else if (!L.wqkv.i8.p && D % 16 == 0 && skinny(H, QKV, T) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
+      // The projection and qkv_post in one launch (the RMSNorm cannot be folded in here).
+      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      RH_CHECK(rh_gemv_f16_qkv(L.wqkv.f16.p, H, xn_.p, qkv_.p, T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab,
+                               kc, vc, q_out, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     } else {
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);

@@ -65,6 +65,67 @@ def test_row_stride_gives_the_same_bits(torch_mod, dev):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def run_split(torch, dev, w, x, ks, beta=0.0, y0=None, ws=None, counters=None):
+    """rh_gemv_f16_splitk; returns y and the counters after the call."""
+    from relay_amd import _lib
+
+    N, K = w.shape
+    T = x.shape[0]
+    W = torch.from_numpy(np.ascontiguousarray(w).view(np.int16)).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    Y = torch.from_numpy(y0.copy()).to(dev) if y0 is not None else torch.full((T, N), float("nan"), device=dev)
+    ws = torch.full((ks * T * N,), float("nan"), device=dev) if ws is None else ws
+    counters = torch.zeros((N + 15) // 16, dtype=torch.int32, device=dev) if counters is None else counters
+    print(f"gemv_f16_splitk case: T={T} K={K} N={N} ksplit={ks} beta={beta}", flush=True)
+    _lib.check(_lib.lib().rh_gemv_f16_splitk(W.data_ptr(), K, X.data_ptr(), Y.data_ptr(), T, K, N, beta, ks,
+                                             ws.data_ptr(), counters.data_ptr(), None), "rh_gemv_f16_splitk")
+    torch.cuda.synchronize()
+    return Y.cpu().numpy(), counters.cpu().numpy()
+
+
+@pytest.mark.parametrize("ks", [1, 2, 3, 8])
+@pytest.mark.parametrize("T,N,K", [(1, 2048, 5632), (32, 2048, 5632), (17, 100, 1024), (5, 33, 512)])
+def test_split_k_matches_float64(torch_mod, dev, T, N, K, ks):
+    """Any K split stays within the fp32 accumulation bound; ksplit 1 is rh_gemv_f16 bit for
+    bit; the counters are back at zero after the call."""
+    w, x = make(N, K, T, seed=T + N + K + ks)
+    y, cnt = run_split(torch_mod, dev, w, x, ks)
+    check(y, w, x)
+    assert (cnt == 0).all()
+    if ks == 1:
+        assert np.array_equal(y.view(np.uint32), run(torch_mod, dev, w, x).view(np.uint32))
+
+
+def test_split_k_repeats_and_accumulates(torch_mod, dev):
+    """The same workspace and counters over calls of different shapes: every call merges its
+    own partials (same bits on a repeat), and beta != 0 adds the old y once."""
+    ws = torch_mod.full((4 * 32 * 2048,), float("nan"), device=dev)
+    counters = torch_mod.zeros(128, dtype=torch_mod.int32, device=dev)
+    w, x = make(2048, 4096, 32, seed=11)
+    a, _ = run_split(torch_mod, dev, w, x, 4, ws=ws, counters=counters)
+    w2, x2 = make(1000, 1024, 3, seed=12)
+    y0 = np.random.default_rng(3).standard_normal((3, 1000)).astype(np.float32)
+    c, cnt = run_split(torch_mod, dev, w2, x2, 2, beta=1.0, y0=y0, ws=ws, counters=counters)
+    check(c, w2, x2, beta=1.0, y0=y0)
+    b, cnt = run_split(torch_mod, dev, w, x, 4, ws=ws, counters=counters)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and (cnt == 0).all()
+
+
+def test_split_plan_and_limits(torch_mod, dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_f16_split_plan(32, 5632, 2048) == 2
+    assert L.rh_gemv_f16_split_plan(32, 2048, 2048) == 1
+    assert L.rh_gemv_f16_split_plan(1, 4096, 14336) == 1
+    assert L.rh_gemv_f16_splitk(None, 64, None, None, 1, 64, 64, 0.0, 9, None, None, None) != 0
+    assert "ksplit must be in 1..8" in _lib.last_error()
+    assert L.rh_gemv_f16_splitk(None, 128, None, None, 1, 128, 64, 0.0, 3, None, None, None) != 0
+    assert "more K ranges" in _lib.last_error()
+    assert L.rh_gemv_f16_splitk(None, 128, None, None, 1, 128, 64, 0.0, 2, None, None, None) != 0
+    assert "workspace" in _lib.last_error()
+
+
 def test_rejects_bad_shapes(torch_mod, dev):
     from relay_amd import _lib
 
@@ -128,11 +189,13 @@ def test_fused_limits(torch_mod, dev):
     assert "LDS" in _lib.last_error()
 
 
-@pytest.mark.parametrize("T,heads,kvh,D,H,bs,with_bias", [(1, 9, 3, 64, 576, 16, False), (15, 32, 4, 64, 2048, 16, True),
-                                                         (5, 32, 8, 128, 4096, 16, False), (20, 8, 2, 64, 320, 12, True),
-                                                         (3, 4, 4, 16, 64, 1, True)])
-def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias):
-    """rh_gemv_f16_rmsnorm_qkv against rh_rmsnorm -> rh_gemv_f16 -> rh_qkv_post.
+@pytest.mark.parametrize("T,heads,kvh,D,H,bs,with_bias,norm", [
+    (1, 9, 3, 64, 576, 16, False, True), (15, 32, 4, 64, 2048, 16, True, True), (5, 32, 8, 128, 4096, 16, False, True),
+    (20, 8, 2, 64, 320, 12, True, True), (3, 4, 4, 16, 64, 1, True, True),
+    (32, 32, 4, 64, 2048, 16, False, False), (17, 9, 3, 64, 576, 16, True, False), (2, 32, 8, 128, 4096, 16, False, False)])
+def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias, norm):
+    """rh_gemv_f16_rmsnorm_qkv (norm) or rh_gemv_f16_qkv (x already normalised) against
+    rh_rmsnorm -> rh_gemv_f16 -> rh_qkv_post.
     Without rotation (inv_freq = 0) every byte of qkv, q and both caches is equal: same sums,
     same placement. With RoPE the two kernels' inlined sincosf/products round differently in
     the last bit (measured: ~20% of rotated values 1 ulp apart), so rotated fp32 values must
@@ -143,7 +206,7 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
     L = _lib.lib()
     rng = np.random.default_rng(T * 31 + D + H)
     N = (heads + 2 * kvh) * D
-    assert L.rh_gemv_f16_fused_fits(T, H)
+    assert not norm or L.rh_gemv_f16_fused_fits(T, H)
     pos = [int(p) for p in rng.permutation(5 * bs + 3)[:T]]  # distinct: one writer per cache slot
     seq = [t % 2 for t in range(T)]
     per = (5 * bs + 3) // bs + 1
@@ -163,14 +226,18 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
         vc = kc.clone()
         qo = torch.zeros(T * heads * D, dtype=torch.int16, device=dev)
         qkv = torch.full((T, N), float("nan"), device=dev)
-        if fused:
+        xn = torch.empty((T, H), dtype=torch.int16, device=dev)
+        _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
+        if fused and not norm:
+            _lib.check(L.rh_gemv_f16_qkv(W.data_ptr(), H, xn.data_ptr(), qkv.data_ptr(), T, H, bp, inv.data_ptr(),
+                                         P.data_ptr(), S.data_ptr(), TO.data_ptr(), TB.data_ptr(), kc.data_ptr(),
+                                         vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs, None), "rh_gemv_f16_qkv")
+        elif fused:
             _lib.check(L.rh_gemv_f16_rmsnorm_qkv(W.data_ptr(), H, x.data_ptr(), nw.data_ptr(), 1e-5, qkv.data_ptr(), T, H,
                                                  bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
                                                  TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh,
                                                  D, bs, None), "rh_gemv_f16_rmsnorm_qkv")
         else:
-            xn = torch.empty((T, H), dtype=torch.int16, device=dev)
-            _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
             _lib.check(L.rh_gemv_f16(W.data_ptr(), H, xn.data_ptr(), qkv.data_ptr(), T, H, N, 0.0, None), "rh_gemv_f16")
             _lib.check(L.rh_qkv_post(qkv.data_ptr(), T, bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
                                      TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs,
@@ -178,7 +245,7 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
         torch.cuda.synchronize()
         return [a.cpu().numpy() for a in (qkv, kc, vc, qo)]
 
-    print(f"fused qkv: T={T} heads={heads}/{kvh} D={D} H={H} bs={bs} bias={with_bias}", flush=True)
+    print(f"fused qkv: T={T} heads={heads}/{kvh} D={D} H={H} bs={bs} bias={with_bias} norm={norm}", flush=True)
     inv0 = dt(np.zeros(D // 2, np.float32))
     for name, a, b in zip(("qkv", "k cache", "v cache", "q"), run(False, inv0), run(True, inv0)):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
