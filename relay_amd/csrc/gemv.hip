@@ -325,8 +325,22 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
   if (PRO == kRmsNorm) {
     const float* xf = static_cast<const float*>(xin);
+    // The staged values' inputs (x and norm_w of this thread's elements) are loaded with the
+    // sums' loads, so the prologue waits for one round of loads instead of three.
+    constexpr int kPre = 4;
+    const bool pre = T * K <= kPre * WAVES * kWave;
+    float px[kPre], pw[kPre];
+    if (pre) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j) {
+        const int idx = threadIdx.x + j * WAVES * kWave;
+        px[j] = idx < T * K ? xf[idx] : 0.0f;
+        pw[j] = idx < T * K ? norm_w[idx % K] : 0.0f;
+      }
+    }
     for (int t = w; t < T; t += WAVES) {
       double ss = 0;
+#pragma unroll 8
       for (int i = lane; i < K; i += kWave) ss += static_cast<double>(xf[static_cast<int64_t>(t) * K + i]) *
                                                  xf[static_cast<int64_t>(t) * K + i];
 #pragma unroll
@@ -334,13 +348,26 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
       if (lane == 0) s_inv[t] = 1.0f / sqrtf(static_cast<float>(ss / K) + eps);
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
-      const int t = idx / K, i = idx - t * K;
-      sxb[t * XR + i] = f16_of_product(norm_w[i], xf[static_cast<int64_t>(t) * K + i] * s_inv[t]);
+    if (pre) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j) {
+        const int idx = threadIdx.x + j * WAVES * kWave;
+        if (idx < T * K) {
+          const int t = idx / K, i = idx - t * K;
+          sxb[t * XR + i] = f16_of_product(pw[j], px[j] * s_inv[t]);
+        }
+      }
+    } else {
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
+        const int t = idx / K, i = idx - t * K;
+        sxb[t * XR + i] = f16_of_product(norm_w[i], xf[static_cast<int64_t>(t) * K + i] * s_inv[t]);
+      }
     }
     __syncthreads();
   } else if (PRO == kSiluMul) {
     const float* gu = static_cast<const float*>(xin);
+#pragma unroll 4
     for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
       const int t = idx / K, i = idx - t * K;
       const float v = gu[static_cast<int64_t>(t) * 2 * K + i];
