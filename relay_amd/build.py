@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["decode_attention.hip", "flash_prefill.hip", "gemv.hip", "gemm_w8.hip", "layer_ops.hip"]
-HOST_SOURCES = ["host/hip_backend.cpp", "host/capi.cpp", "host/config.cpp", "host/backend_defaults.cpp"]
+HOST_SOURCES = ["host/hip_backend.cpp", "host/lt_gemm.cpp", "host/capi.cpp", "host/config.cpp", "host/backend_defaults.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter",
@@ -61,7 +61,7 @@ def build(verbose: bool = False) -> str:
                 print(" ".join(cmd), flush=True)
         list(ex.map(_run, jobs))
     tmp = LIB + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp, f"-L{ROCM}/lib", "-lrocblas",
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp, f"-L{ROCM}/lib", "-lhipblaslt", "-lrocblas",
           "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp, LIB)
     return LIB

@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <mutex>
 #include <numeric>
 #include <stdexcept>
@@ -31,6 +32,7 @@
 #include "relay/backend.h"
 #include "relay_hip.h"
 #include "host_common.h"
+#include "lt_gemm.h"
 
 namespace relay {
 
@@ -45,6 +47,7 @@ namespace {
 
 using relay_hip_host::DeviceArray;
 using relay_hip_host::PinnedBuffer;
+using relay_hip_host::LtGemm;
 
 
 #define ROCBLAS_CHECK(x)                                                                          \
@@ -93,6 +96,9 @@ class HipBackend final : public Backend {
     HIP_CHECK(hipEventCreate(&fwd_end_));
     ROCBLAS_CHECK(rocblas_create_handle(&blas_));
     ROCBLAS_CHECK(rocblas_set_stream(blas_, stream_));
+    // RELAY_HIP_GEMM=rocblas keeps every library product on rocBLAS' own choice.
+    const char* g = std::getenv("RELAY_HIP_GEMM");
+    if (!(g && std::string(g) == "rocblas")) lt_ = std::make_unique<LtGemm>(stream_);
     layer_done_.resize(c_.layers);
     for (auto& e : layer_done_) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     layout_ = {c_.layers, c_.kv_heads, c_.head_dim, block_size, num_blocks};
@@ -192,6 +198,7 @@ class HipBackend final : public Backend {
   int max_tokens_, max_context_, device_;
   hipStream_t stream_ = nullptr, copy_stream_ = nullptr;
   rocblas_handle blas_ = nullptr;
+  std::unique_ptr<LtGemm> lt_;  // timed-choice hipBLASLt products (rocBLAS if it has none)
   std::vector<hipEvent_t> layer_done_;
   hipEvent_t fwd_begin_ = nullptr, fwd_end_ = nullptr;
   double last_ms_ = 0;
@@ -352,6 +359,10 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
     RH_CHECK(rh_gemv_f16_splitk(W, K, x, y, T, K, N, beta, ks, split_ws_.p, split_counters_.p, stream_));
     return;
   }
+  // Library products of the fp16 weights: hipBLASLt with a timed choice. A dequantized int8
+  // copy (just written, read from the caches) stays on rocBLAS: measured faster there
+  // (Llama-3 int8 mixed step 26.0 vs 26.7 ms).
+  if (lt_ && W != dequant_.p && lt_->run(W, x, y, T, K, N, beta)) return;
   // Row-major y[T, N] = x[T, K] W[N, K]^T is column-major y^T (N x T) = W^T-view (K x N)^T x^T.
   const float alpha = 1.0f;
   ROCBLAS_CHECK(rocblas_gemm_ex(blas_, rocblas_operation_transpose, rocblas_operation_none, N, T, K, &alpha, W,

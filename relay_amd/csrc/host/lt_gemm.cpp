@@ -1,0 +1,145 @@
+// hipBLASLt products with the algorithm chosen by timing (see lt_gemm.h).
+#include "lt_gemm.h"
+
+#include <hipblaslt/hipblaslt-ext.hpp>
+
+#include <stdexcept>
+#include <string>
+
+namespace relay_hip_host {
+
+namespace {
+
+#define LT_CHECK(x)                                                                          \
+  do {                                                                                       \
+    hipblasStatus_t _s = (x);                                                                \
+    if (_s != HIPBLAS_STATUS_SUCCESS)                                                        \
+      throw std::runtime_error(std::string("hipBLASLt: status ") + std::to_string(_s) + " at " #x); \
+  } while (0)
+
+// Token counts share a tuned algorithm within powers of two.
+int bucket(int T) {
+  int b = 1;
+  while (b < T) b <<= 1;
+  return b;
+}
+
+}  // namespace
+
+LtGemm::LtGemm(hipStream_t stream) : stream_(stream), workspace_(kWorkspaceBytes) {
+  LT_CHECK(hipblasLtCreate(&handle_));
+  HIP_CHECK(hipEventCreate(&ev_[0]));
+  HIP_CHECK(hipEventCreate(&ev_[1]));
+}
+
+LtGemm::~LtGemm() {
+  for (auto& kv : shapes_) {
+    Shape& s = *kv.second;
+    if (s.a) hipblasLtMatrixLayoutDestroy(s.a);
+    if (s.b) hipblasLtMatrixLayoutDestroy(s.b);
+    if (s.c) hipblasLtMatrixLayoutDestroy(s.c);
+    if (s.desc) hipblasLtMatmulDescDestroy(s.desc);
+  }
+  for (hipEvent_t e : ev_)
+    if (e) (void)hipEventDestroy(e);
+  if (handle_) hipblasLtDestroy(handle_);
+}
+
+bool LtGemm::supported(Shape& s, hipblasLtMatmulAlgo_t& algo) {
+  const float alpha = 1.0f, beta = 0.0f;
+  std::size_t ws = 0;
+  return hipblaslt_ext::matmulIsAlgoSupported(handle_, s.desc, &alpha, s.a, s.b, &beta, s.c, s.c, algo, ws) ==
+             HIPBLAS_STATUS_SUCCESS &&
+         ws <= kWorkspaceBytes;
+}
+
+// Row-major y[T, N] = x[T, K] W[N, K]^T is column-major y^T (N x T) = op(A) B with A the
+// K x N column-major view of W (transposed) and B the K x T view of x.
+LtGemm::Shape& LtGemm::shape(const void* W, const void* x, int T, int K, int N) {
+  auto key = std::make_tuple(T, N, K);
+  auto it = shapes_.find(key);
+  if (it != shapes_.end()) return *it->second;
+  auto s = std::make_unique<Shape>();
+  LT_CHECK(hipblasLtMatmulDescCreate(&s->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  LT_CHECK(hipblasLtMatmulDescSetAttribute(s->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)));
+  LT_CHECK(hipblasLtMatmulDescSetAttribute(s->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&s->a, HIP_R_16F, K, N, K));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&s->b, HIP_R_16F, K, T, K));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&s->c, HIP_R_32F, N, T, N));
+  // The bucket's tuned algorithm if it serves this exact shape, else tune on this shape.
+  const auto bkey = std::make_tuple(bucket(T), N, K);
+  auto t = tuned_.find(bkey);
+  if (t != tuned_.end() && supported(*s, t->second)) {
+    s->algo = t->second;
+    s->valid = true;
+  } else {
+    hipblasLtMatmulAlgo_t best{};
+    s->valid = tune(*s, W, x, T, K, N, best);
+    if (s->valid) {
+      s->algo = best;
+      if (t == tuned_.end()) tuned_.emplace(bkey, best);
+    }
+  }
+  return *shapes_.emplace(key, std::move(s)).first->second;
+}
+
+bool LtGemm::tune(Shape& s, const void* W, const void* x, int T, int K, int N, hipblasLtMatmulAlgo_t& best) {
+  hipblasLtMatmulPreference_t pref;
+  LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
+  const uint64_t ws = kWorkspaceBytes;
+  LT_CHECK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)));
+  hipblasLtMatmulHeuristicResult_t res[kCandidates];
+  int n = 0;
+  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle_, s.desc, s.a, s.b, s.c, s.c, pref, kCandidates,
+                                                             res, &n);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (st != HIPBLAS_STATUS_SUCCESS || n <= 0) return false;
+  const std::size_t need = static_cast<std::size_t>(T) * N;
+  if (need > scratch_.n) scratch_ = DeviceArray<float>(need);
+  // Each timed call starts with W out of the caches, as in a forward pass (every layer's
+  // weights are new): timing on cache-resident weights favours other kernels.
+  DeviceArray<unsigned char> flush(kFlushBytes);
+  const float alpha = 1.0f, beta = 0.0f;
+  float best_ms = 0.0f;
+  int chosen = -1;
+  for (int i = 0; i < n; ++i) {
+    if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspaceBytes) continue;
+    auto call = [&] {
+      return hipblasLtMatmul(handle_, s.desc, &alpha, W, s.a, x, s.b, &beta, scratch_.p, s.c, scratch_.p, s.c,
+                             &res[i].algo, workspace_.p, kWorkspaceBytes, stream_);
+    };
+    if (call() != HIPBLAS_STATUS_SUCCESS) continue;
+    constexpr int kReps = 3;
+    bool ok = true;
+    float ms = 0.0f;
+    for (int r = 0; r < kReps && ok; ++r) {
+      HIP_CHECK(hipMemsetAsync(flush.p, r, kFlushBytes, stream_));
+      HIP_CHECK(hipEventRecord(ev_[0], stream_));
+      ok = call() == HIPBLAS_STATUS_SUCCESS;
+      HIP_CHECK(hipEventRecord(ev_[1], stream_));
+      HIP_CHECK(hipEventSynchronize(ev_[1]));
+      float one = 0.0f;
+      HIP_CHECK(hipEventElapsedTime(&one, ev_[0], ev_[1]));
+      ms += one;
+    }
+    if (ok && (chosen < 0 || ms < best_ms)) {
+      best_ms = ms;
+      chosen = i;
+    }
+  }
+  if (chosen < 0) return false;
+  best = res[chosen].algo;
+  return true;
+}
+
+bool LtGemm::run(const void* W, const void* x, float* y, int T, int K, int N, float beta) {
+  Shape& s = shape(W, x, T, K, N);
+  if (!s.valid) return false;
+  const float alpha = 1.0f;
+  LT_CHECK(hipblasLtMatmul(handle_, s.desc, &alpha, W, s.a, x, s.b, &beta, y, s.c, y, s.c, &s.algo, workspace_.p,
+                           kWorkspaceBytes, stream_));
+  return true;
+}
+
+}  // namespace relay_hip_host
