@@ -519,10 +519,14 @@ int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x,
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
-  if (T <= 16) return launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
-  // Two row tiles per workgroup only while that still leaves >= 192 workgroups (measured at
-  // T = 17-64: N = 6144 gains up to 30%, N = 4096 with 128 workgroups loses as much).
+  // Two row tiles per workgroup (sharing the activation operands, half the activation
+  // traffic through L2) only while that still leaves >= 192 workgroups: measured at T = 17-64,
+  // N = 6144 gains up to 30% and N = 4096 with 128 workgroups loses as much; at T = 4-16 on
+  // N = 14336, 17.1 -> 16.5 us (T = 4), 19.6 -> 17.8 (8), 26.0 -> 20.9 (16), while at T <= 2
+  // or on N <= 4096 it is level or slower.
   const bool tall = (N + 31) / 32 >= 192;
+  if (T <= 16) return tall && T >= 4 ? launch_nb<1, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
+                                     : launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
   if (T <= 32) return tall ? launch_nb<2, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
                            : launch_nb<2, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
   if (T <= 48) return tall ? launch_nb<3, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
