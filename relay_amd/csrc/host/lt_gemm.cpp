@@ -99,7 +99,12 @@ bool LtGemm::tune(Shape& s, const void* W, const void* x, int T, int K, int N, h
   if (need > scratch_.n) scratch_ = DeviceArray<float>(need);
   // Each timed call starts with W out of the caches, as in a forward pass (every layer's
   // weights are new): timing on cache-resident weights favours other kernels.
-  DeviceArray<unsigned char> flush(kFlushBytes);
+  // (Without the memory for it, the candidates are timed as they come.)
+  void* flush = nullptr;
+  if (hipMalloc(&flush, kFlushBytes) != hipSuccess) {
+    flush = nullptr;
+    (void)hipGetLastError();
+  }
   const float alpha = 1.0f, beta = 0.0f;
   float best_ms = 0.0f;
   int chosen = -1;
@@ -114,7 +119,7 @@ bool LtGemm::tune(Shape& s, const void* W, const void* x, int T, int K, int N, h
     bool ok = true;
     float ms = 0.0f;
     for (int r = 0; r < kReps && ok; ++r) {
-      HIP_CHECK(hipMemsetAsync(flush.p, r, kFlushBytes, stream_));
+      if (flush) HIP_CHECK(hipMemsetAsync(flush, r, kFlushBytes, stream_));
       HIP_CHECK(hipEventRecord(ev_[0], stream_));
       ok = call() == HIPBLAS_STATUS_SUCCESS;
       HIP_CHECK(hipEventRecord(ev_[1], stream_));
@@ -128,6 +133,7 @@ bool LtGemm::tune(Shape& s, const void* W, const void* x, int T, int K, int N, h
       chosen = i;
     }
   }
+  if (flush) HIP_CHECK(hipFree(flush));
   if (chosen < 0) return false;
   best = res[chosen].algo;
   return true;

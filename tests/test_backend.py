@@ -191,3 +191,36 @@ def test_errors_follow_relay_conventions(dev):
     with pytest.raises(ValueError):  # longer than max_context
         be.forward(ForwardBatch([SeqChunk([1], 100, list(range(7)), True)]))
     assert be.forward(ForwardBatch([])).shape[0] == 0
+
+
+def test_library_gemm_choices_agree(dev, monkeypatch):
+    """Prompts above the skinny product's token range run their projections as library GEMMs:
+    hipBLASLt with a timed kernel choice by default, rocBLAS' own choice with
+    RELAY_HIP_GEMM=rocblas. Both are fp32 sums of the same fp16 products, so the logits agree
+    to accumulation-order rounding and the greedy tokens are the same; both stay within 2e-3
+    of the CPU oracle."""
+    w = small_model(64, 8, 2, layers=2, hidden=512, inter=1024, vocab=1024, std=0.05, seed=5)
+    for L in w.layers:  # fp16 values, so the oracle and the GPU see the same weights
+        for f in ("attn_norm", "wqkv", "wo", "mlp_norm", "w_gate_up", "w_down"):
+            a = getattr(L, f)
+            np.copyto(a, a.astype(np.float16).astype(np.float32))
+    for a in (w.embed, w.lm_head, w.final_norm):
+        if a is not None:
+            np.copyto(a, a.astype(np.float16).astype(np.float32))
+    prompt = list(np.random.default_rng(1).integers(0, 1024, size=200))
+    b = ForwardBatch([SeqChunk(prompt, 0, list(range(13)), True)], all_logits=True)
+    got = {}
+    for mode in ("default", "rocblas"):
+        if mode == "rocblas":
+            monkeypatch.setenv("RELAY_HIP_GEMM", "rocblas")
+        else:
+            monkeypatch.delenv("RELAY_HIP_GEMM", raising=False)
+        print(f"library gemm mode {mode}: T={len(prompt)}", flush=True)
+        be = HipBackend(w, 16, 16, max_batch_tokens=256, options=FAST)
+        got[mode] = be.forward(b)
+        be.close()
+    cpu = O.CpuBackend(w, 16, 16).forward(b)
+    assert rel_err_rowmax(got["default"], got["rocblas"]) < 1e-3
+    assert (got["default"].argmax(axis=1) == got["rocblas"].argmax(axis=1)).mean() >= 0.98
+    for mode in got:
+        assert rel_err_rowmax(got[mode], cpu) < 2e-3, mode
