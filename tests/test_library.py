@@ -133,3 +133,29 @@ def test_prefill_plan_rejects_small_capacity():
     assert _lib.lib().rh_prefill_plan(a.ctypes.data, n.ctypes.data, a.ctypes.data, a.ctypes.data, 1, 4,
                                       work.ctypes.data, 1) < 0
     assert "capacity" in _lib.last_error()
+
+
+def test_work_planners_follow_their_rules():
+    """The host-side planners (no device needed): rh_decode_slice_keys cuts contexts into
+    whole chunks, one slice for a handful of short contexts, at least two otherwise, never
+    below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles;
+    rh_gemv_int8_row_stride pads rows that are a multiple of 2 KB."""
+    L = _lib.lib()
+    for D in (64, 128):
+        chunk = L.rh_decode_chunk_keys(D)
+        assert chunk == (64 if D == 64 else 32)
+        for n, kvh, g, ctx in [(32, 4, 8, 2048), (48, 8, 4, 8192), (1, 3, 3, 640), (1, 8, 4, 65536), (200, 8, 4, 100)]:
+            sk = L.rh_decode_slice_keys(n, kvh, g, D, ctx)
+            assert sk > 0 and sk % chunk == 0
+            groups = n * kvh * ((g + 15) // 16)
+            if groups <= 16 and ctx <= 16 * chunk:
+                assert sk >= ctx  # one slice
+            else:
+                assert sk >= 8 * chunk and (ctx + sk - 1) // sk >= min(2, (ctx + 8 * chunk - 1) // (8 * chunk))
+    assert L.rh_decode_slice_keys(32, 4, 8, 64, 2048) == 1024  # config 2: two slices of 1024 keys
+    assert L.rh_decode_chunk_keys(96) == -1
+    assert [L.rh_gemv_f16_split_plan(T, K, N) for T, K, N in
+            [(32, 5632, 2048), (1, 5632, 2048), (32, 2048, 2048), (32, 4096, 4096), (8, 14336, 4096), (1, 4096, 1024)]] \
+        == [2, 2, 1, 1, 1, 2]
+    assert L.rh_gemv_f16_split_plan(0, 64, 64) == -1
+    assert [L.rh_gemv_int8_row_stride(K) for K in (4096, 14336, 2048, 576, 100)] == [4352, 14592, 2304, 576, 112]
