@@ -206,6 +206,19 @@ int rh_gemv_f16_max_tokens(void);
 int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
                float beta, void* stream);
 
+/* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 64-token tile and K cut into ksplit ranges
+ * (1 <= ksplit <= 8, at most one per step of 128 k, or of 64 k when K is not a multiple
+ * of 128), so that decode batches of 17-64 tokens read the int8
+ * weights once on enough workgroups. ksplit > 1 writes each range's raw sums to workspace
+ * (fp32, ksplit * T * N values, N a multiple of 4) and a second launch adds them in range
+ * order before the scale and beta (deterministic). Calls sharing a workspace must not
+ * overlap. No counterpart in relay (dequantize + cublasGemmEx, cuda_backend.cu:718-722). */
+int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
+                      float beta, int ksplit, float* workspace, void* stream);
+
+/* The ksplit rh_gemm_w8_skinny uses for this shape (-1 outside its limits). */
+int rh_gemm_w8_split_plan(int T, int K, int N);
+
 /* Per-row symmetric int8 quantization of an fp32 matrix [N, K] on the device:
  * scale[n] = max_k |w[n, k]| / 127 (1 if the row is all zero), q = round-half-even(w / scale),
  * q rows ldq bytes apart (ldq >= K; the bytes past K are not written).

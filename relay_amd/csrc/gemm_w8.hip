@@ -58,11 +58,19 @@ struct Tile {
   static constexpr int kPieces = kToks * kPR / kThreads;  // 16-byte activation pieces per thread
 };
 
+// Split K (gridDim.z > 1): each workgroup takes a range of K steps and writes its raw sums
+// to ws [ksn][T][N]; w8_split_merge_kernel then adds the ranges in order and applies the
+// scale and beta (a second launch: a merge inside this kernel by the last workgroup to
+// arrive needed registers that cut the main loop's occupancy from 4 waves per SIMD to 1).
+struct W8Split {
+  float* ws;
+};
+
 template <int WN, int WT, int AN, int BT, int KS, int PF>
 __global__ __launch_bounds__(64 * WN * WT) void gemm_w8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                               const float* __restrict__ scale,
                                                               const half_t* __restrict__ x, float* y, int T, int K,
-                                                              int N, float beta) {
+                                                              int N, float beta, W8Split sp) {
   using TL = Tile<WN, WT, AN, BT, KS>;
   constexpr int kXRow = TL::kXRow, kPR = TL::kPR, kWV = TL::kWV;
   __shared__ __attribute__((aligned(16))) half_t xs[2][TL::kToks * kXRow];
@@ -73,7 +81,8 @@ __global__ __launch_bounds__(64 * WN * WT) void gemm_w8_kernel(const int8_t* __r
 #pragma unroll
   for (int a = 0; a < AN; ++a)
     wp[a] = w8 + static_cast<int64_t>(min(n0 + 32 * (AN * wn + a) + c, N - 1)) * ldw + (KS / 2) * h;
-  const int nsteps = K / KS;
+  const int ksn = gridDim.z, kz = blockIdx.z;
+  const int nall = K / KS, sbeg = kz * nall / ksn, nsteps = (kz + 1) * nall / ksn - sbeg;
 
   // Activation loader: thread tid moves 16-byte pieces e = tid + kThreads j of the tile
   // (token e / kPR, k piece e % kPR). Tokens past T re-read row T - 1: a token's column of
@@ -89,7 +98,7 @@ __global__ __launch_bounds__(64 * WN * WT) void gemm_w8_kernel(const int8_t* __r
   uint4v wr[PF][AN][kWV];
   half8 xr[PF][TL::kPieces];
   auto load = [&](int s, int u) {
-    const int k0 = s * KS;
+    const int k0 = (sbeg + s) * KS;
 #pragma unroll
     for (int a = 0; a < AN; ++a)
 #pragma unroll
@@ -150,6 +159,24 @@ __global__ __launch_bounds__(64 * WN * WT) void gemm_w8_kernel(const int8_t* __r
 
   // Accumulator register i of lane (c, h) holds row 8 (i / 4) + 4 h + i % 4 of its 32-row
   // block, for token column c.
+  if (ksn > 1) {
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      const int t = t0 + 32 * (BT * wt + b) + c;
+      if (t >= T) continue;
+      float* wr = sp.ws + (static_cast<int64_t>(kz) * T + t) * N;
+#pragma unroll
+      for (int a = 0; a < AN; ++a)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = n0 + 32 * (AN * wn + a) + 8 * q + 4 * h + r;
+            if (n < N) wr[n] = acc[a][b][4 * q + r];
+          }
+    }
+    return;
+  }
 #pragma unroll
   for (int b = 0; b < BT; ++b) {
     const int t = t0 + 32 * (BT * wt + b) + c;
@@ -169,16 +196,50 @@ __global__ __launch_bounds__(64 * WN * WT) void gemm_w8_kernel(const int8_t* __r
   }
 }
 
+// y[t, n] = scale[n] * sum_z ws[z][t][n] (+ beta y), the ranges added in order; one thread
+// per 4 consecutive n of a token row, all ksn loads in flight.
+constexpr int kMaxW8Split = 8;
+__global__ __launch_bounds__(256) void w8_split_merge_kernel(const float* __restrict__ ws, int ksn, int T, int N,
+                                                             const float* __restrict__ scale, float* y, float beta) {
+  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i4 >= static_cast<int64_t>(T) * N) return;
+  const int64_t plane = static_cast<int64_t>(T) * N;
+  const int n = static_cast<int>(i4 % N);
+  float p[kMaxW8Split][4];
+#pragma unroll
+  for (int z = 0; z < kMaxW8Split; ++z)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[z][e] = z < ksn ? ws[z * plane + i4 + e] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = 0.0f;
+#pragma unroll
+    for (int z = 0; z < kMaxW8Split; ++z)
+      if (z < ksn) v += p[z][e];
+    const float o = v * scale[n + e];
+    y[i4 + e] = o + (beta != 0.0f ? beta * y[i4 + e] : 0.0f);
+  }
+}
+
 template <int WN, int WT, int AN, int BT, int KS, int PF>
 int launch_w8(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K, int N,
-              float beta, hipStream_t s) {
+              float beta, hipStream_t s, int ksplit = 1, W8Split sp = W8Split{}) {
   using TL = Tile<WN, WT, AN, BT, KS>;
-  const dim3 grid((N + TL::kRows - 1) / TL::kRows, (T + TL::kToks - 1) / TL::kToks);
+  const dim3 grid((N + TL::kRows - 1) / TL::kRows, (T + TL::kToks - 1) / TL::kToks, ksplit);
   RH_REQUIRE(grid.y <= 65535, "gemm_w8: T too large");
   RH_TRY_LAUNCH(hipLaunchKernelGGL((gemm_w8_kernel<WN, WT, AN, BT, KS, PF>), grid, dim3(TL::kThreads), 0, s, w8, ldw, scale,
-                                   x, y, T, K, N, beta));
+                                   x, y, T, K, N, beta, sp));
+  if (ksplit > 1) {
+    const int64_t quads = static_cast<int64_t>(T) * N / 4;
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_split_merge_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                                     s, sp.ws, ksplit, T, N, scale, y, beta));
+  }
   return 0;
 }
+
+// The tile for 17-64 tokens: 128 rows x 64 tokens, 4 waves of 32 rows (the 128-token tile
+// leaves most MFMA columns idle there and gives 4x fewer row tiles per token).
+constexpr int kSkinnyRows = 128, kSkinnyTokens = 64;
 
 }  // namespace
 }  // namespace relay_hip
@@ -196,5 +257,38 @@ extern "C" int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, con
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
   return launch_w8<2, 2, 1, 2, 64, 1>(w8, ldw, scale, xh, y, T, K, N, beta, st);
-  return 0;
+}
+
+// k per step of the skinny tile: 128 when K allows (measured 10-15% faster than 64 at
+// 32-48 tokens; deeper register prefetch of the weights gained nothing).
+static int skinny_step(int K) { return K % 128 == 0 ? 128 : 64; }
+
+extern "C" int rh_gemm_w8_split_plan(int T, int K, int N) {
+  if (T < 1 || T > kSkinnyTokens || K <= 0 || K % 64 || N <= 0) return -1;
+  // The fewest K ranges that give >= 256 workgroups (one per CU), each range >= 8 steps.
+  // Measured at Llama-3-8B shapes, T = 32-48: N = 4096, K = 14336 best with 8 ranges,
+  // N = 28672, K = 4096 with 2; more ranges than that were slower.
+  const int tiles = (N + kSkinnyRows - 1) / kSkinnyRows, steps = K / skinny_step(K);
+  int ks = 1;
+  while (tiles * ks < 256 && 2 * ks <= kMaxW8Split && steps / (2 * ks) >= 8) ks *= 2;
+  return ks;
+}
+
+extern "C" int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T,
+                                 int K, int N, float beta, int ksplit, float* workspace, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && T <= kSkinnyTokens, "gemm_w8_skinny: T must be in 1..64");
+  RH_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "gemm_w8_skinny: K must be a positive multiple of 64");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemm_w8_skinny: ldw must be >= K and a multiple of 16");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemm_w8_skinny: W8 and x must be 16-byte aligned");
+  RH_REQUIRE(ksplit >= 1 && ksplit <= kMaxW8Split && ksplit <= K / skinny_step(K),
+             "gemm_w8_skinny: ksplit must be in 1..8 and at most the number of k steps");
+  RH_REQUIRE(ksplit == 1 || workspace, "gemm_w8_skinny: ksplit > 1 needs a workspace");
+  RH_REQUIRE(ksplit == 1 || N % 4 == 0, "gemm_w8_skinny: ksplit > 1 needs N a multiple of 4");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const half_t* xh = static_cast<const half_t*>(x);
+  if (skinny_step(K) == 128)
+    return launch_w8<4, 1, 1, 2, 128, 1>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, W8Split{workspace});
+  return launch_w8<4, 1, 1, 2, 64, 1>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, W8Split{workspace});
 }

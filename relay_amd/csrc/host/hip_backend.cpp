@@ -382,11 +382,22 @@ bool HipBackend::fused(const DeviceMatrix& W, int T) const {
 
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
-  // int8 (measured at Llama-3-8B shapes): the GEMV up to 16 tokens; the int8 GEMM for wide
-  // matrices (N >= 16384) up to 256 tokens (3.5x faster than dequantize + GEMM at T = 48);
-  // the GEMV up to 64 tokens on narrower ones; otherwise dequantize + library GEMM (relay's
-  // path for every T above its GEMV limit), which wins once the GEMM is compute-bound.
+  // int8 (measured at Llama-3-8B shapes): the GEMV up to 16 tokens; the split-K int8 GEMM
+  // at 17-64 tokens on wide or long-K matrices; the int8 GEMM for wide matrices
+  // (N >= 16384) up to 256 tokens (3.5x faster than dequantize + GEMM at T = 48); the GEMV
+  // up to 64 tokens on narrower ones; otherwise dequantize + library GEMM (relay's path for
+  // every T above its GEMV limit), which wins once the GEMM is compute-bound.
   const bool wide = W.N >= 16384 && W.K % 64 == 0 && T <= 256;
+  // 17-64 tokens on wide or long-K matrices: the int8 GEMM with the 64-token tile and K cut
+  // into ranges (Llama-3-8B at T = 48: gate_up 64.9 -> 44.2 us, down 47.2 -> 28.6 us); the
+  // GEMV stays ahead on the 4096-6144-row, K = 4096 matrices.
+  if (T > 16 && T <= 64 && W.K % 64 == 0 && W.N % 4 == 0 && (W.N >= 16384 || W.K >= 8192)) {
+    const int ks = rh_gemm_w8_split_plan(T, W.K, W.N);
+    const std::size_t need = static_cast<std::size_t>(ks) * T * W.N;
+    if (ks > 1 && need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
+    RH_CHECK(rh_gemm_w8_skinny(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, split_ws_.p, stream_));
+    return;
+  }
   if (T <= 16 || (T <= rh_gemv_int8_max_tokens() && !wide)) {
     RH_CHECK(rh_gemv_int8(W.i8.p, W.ldw, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
     return;

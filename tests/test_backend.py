@@ -224,3 +224,27 @@ def test_library_gemm_choices_agree(dev, monkeypatch):
     assert (got["default"].argmax(axis=1) == got["rocblas"].argmax(axis=1)).mean() >= 0.98
     for mode in got:
         assert rel_err_rowmax(got[mode], cpu) < 2e-3, mode
+
+
+def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev):
+    """Weights of the form q * 2^-9 with a +-127 in every row quantize exactly (scale 2^-9,
+    the same q back), so the int8 backend multiplies the same values as the fp16 one and the
+    logits may differ only by fp32 summation order (amplified where an activation is rounded
+    to fp16 between layers: measured 2e-4; a wrong product would be off by O(1)). intermediate 8192 and 20 decode
+    sequences put gate_up (N 16384) and down (K 8192) on the split-K int8 GEMM at 20
+    tokens; the prompts (100 tokens) take the dequantize + library GEMM path."""
+    w = small_model(64, 4, 2, layers=1, hidden=256, inter=8192, vocab=512, seed=3)
+    rng = np.random.default_rng(11)
+    for L in w.layers:
+        for f in ("wqkv", "wo", "w_gate_up", "w_down"):
+            a = getattr(L, f)
+            q = rng.integers(-127, 128, size=a.shape).astype(np.float32)
+            q[:, 0] = np.where(rng.random(a.shape[0]) < 0.5, 127.0, -127.0)
+            np.copyto(a, q * 2.0 ** -9)
+    lens = [5] * 20
+    nb = blocks_needed(lens, 4)
+    a = HipBackend(w, nb, 16, max_batch_tokens=2048, options=FAST)
+    b = HipBackend(w, nb, 16, max_batch_tokens=2048, options=HipOptions(False, True))
+    worst, agree, total = compare(a, b, w.config.vocab, lens, 64, 4)
+    print(f"int8 vs fp16, exactly quantizable weights: relative logit difference {worst:.2e}, argmax {agree}/{total}")
+    assert worst < 1e-3 and agree >= total - 1

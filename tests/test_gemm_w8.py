@@ -108,3 +108,52 @@ def test_rejects_bad_shapes(torch_mod, dev):
     assert L.rh_gemm_w8(None, 96, None, None, None, 4, 96, 64, 0.0, None) != 0 and "K must" in _lib.last_error()
     assert L.rh_gemm_w8(None, 72, None, None, None, 4, 64, 64, 0.0, None) != 0 and "ldw" in _lib.last_error()
     assert L.rh_gemm_w8(None, 64, None, None, None, 0, 64, 64, 0.0, None) == 0  # nothing to do
+
+
+def run_skinny(torch, dev, q, scale, x, ks, beta=0.0, y0=None, ldw=None):
+    from relay_amd import _lib
+
+    N, K = q.shape
+    T = x.shape[0]
+    ldw = K if ldw is None else ldw
+    padded = np.full((N, ldw), 99, np.int8)
+    padded[:, :K] = q
+    W = torch.from_numpy(padded).to(dev)
+    S = torch.from_numpy(scale).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    Y = torch.from_numpy(y0.copy()).to(dev) if y0 is not None else torch.full((T, N), float("nan"), device=dev)
+    ws = torch.full((ks * T * N,), float("nan"), device=dev)
+    print(f"gemm_w8_skinny case: T={T} K={K} N={N} ldw={ldw} ksplit={ks} beta={beta}", flush=True)
+    _lib.check(_lib.lib().rh_gemm_w8_skinny(W.data_ptr(), ldw, S.data_ptr(), X.data_ptr(), Y.data_ptr(), T, K, N, beta,
+                                            ks, ws.data_ptr(), None), "rh_gemm_w8_skinny")
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+@pytest.mark.parametrize("ks", [1, 2, 3, 8])
+@pytest.mark.parametrize("T,N,K", [(1, 64, 1024), (17, 200, 2048), (48, 1000, 4096), (64, 4096, 14336 // 4),
+                                   (33, 132, 1088)])
+def test_skinny_split_k_matches_float64(torch_mod, dev, T, N, K, ks):
+    """rh_gemm_w8_skinny at any K split (128-k steps, or 64 for K = 1088) stays within the
+    fp32 bound; the split adds the ranges in order, so a repeat gives the same bits."""
+    q, scale, x = make(N, K, T, seed=T + N + K + ks)
+    y = run_skinny(torch_mod, dev, q, scale, x, ks)
+    check(y, q, scale, x)
+    assert np.array_equal(y.view(np.uint32), run_skinny(torch_mod, dev, q, scale, x, ks).view(np.uint32))
+
+
+def test_skinny_accumulates_and_limits(torch_mod, dev):
+    from relay_amd import _lib
+
+    q, scale, x = make(300, 2048, 40, seed=9)
+    y0 = np.random.default_rng(4).standard_normal((40, 300)).astype(np.float32)
+    check(run_skinny(torch_mod, dev, q, scale, x, 4, beta=1.0, y0=y0), q, scale, x, beta=1.0, y0=y0)
+    L = _lib.lib()
+    assert L.rh_gemm_w8_split_plan(48, 14336, 4096) == 8 and L.rh_gemm_w8_split_plan(48, 4096, 28672) == 2
+    assert L.rh_gemm_w8_split_plan(65, 4096, 4096) == -1
+    assert L.rh_gemm_w8_skinny(None, 128, None, None, None, 65, 128, 64, 0.0, 1, None, None) != 0
+    assert "T must be in 1..64" in _lib.last_error()
+    assert L.rh_gemm_w8_skinny(None, 128, None, None, None, 8, 128, 64, 0.0, 2, None, None) != 0
+    assert "ksplit" in _lib.last_error()
+    assert L.rh_gemm_w8_skinny(None, 256, None, None, None, 8, 256, 64, 0.0, 2, None, None) != 0
+    assert "workspace" in _lib.last_error()
