@@ -334,6 +334,43 @@ def bench_llama3_mixed(steps, int8=False, n_dec=48, ctx=8192, chunk=512):
             "roofline_ms": round(roof_ms, 2), "frac_roofline": round(roof_ms / dev_ms, 4)}
 
 
+def bench_kv_io(steps=5, ctx=8192):
+    """The KV-I/O half of the boundary (relay's KVSender / KVReceiver calls): read_kv_layer
+    and write_kv_layer of one sequence's blocks (Llama-3-8B layer shape, ctx positions) to
+    and from host memory, through the gather/scatter kernels and pinned staging on the copy
+    stream. Host-inclusive GB/s of the 2 * blocks * kv_block_bytes moved per call; the round
+    trip is checked byte for byte."""
+    import dataclasses
+
+    from relay_amd import HipBackend, HipOptions, llama3_8b
+
+    c = dataclasses.replace(llama3_8b(), layers=2)
+    bs = 16
+    n = ctx // bs + 1
+    nb = 2 * n + 7
+    be = HipBackend(None, nb, bs, max_batch_tokens=64, config=c, synthetic_seed=0, synthetic_std=0.02,
+                    options=HipOptions(False, False))
+    be.fill_kv_random(seed=5, std=1.0)
+    blocks = np.random.default_rng(3).permutation(nb)[:n].tolist()
+    nbytes = 2 * n * be.kv_block_bytes()
+    data = be.read_kv_layer(1, blocks)  # into a buffer the caller keeps (as the engine's sender does)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        be.read_kv_layer(1, blocks, out=data)
+    rd = (time.perf_counter() - t0) / steps
+    other = np.random.default_rng(4).permutation(nb)[:n].tolist()
+    be.write_kv_layer(0, other, data)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        be.write_kv_layer(0, other, data)
+    be.wait_kv_written(0)
+    wr = (time.perf_counter() - t0) / steps
+    same = bool(np.array_equal(be.read_kv_layer(0, other), data))
+    be.close()
+    return {"blocks": n, "bytes": nbytes, "read_ms": round(rd * 1e3, 3), "read_gbs": round(nbytes / rd / 1e9, 1),
+            "write_ms": round(wr * 1e3, 3), "write_gbs": round(nbytes / wr / 1e9, 1), "round_trip_exact": same}
+
+
 # ---- CPU baseline ----------------------------------------------------------------------
 
 def cpu_baseline(sample_seqs=8, ctx=2048, heads=32, kvh=4, D=64, bs=16):
@@ -388,7 +425,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--leg", choices=["prefill", "prefill128", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
+    ap.add_argument("--leg", choices=["prefill", "prefill128", "kvio", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
                                            "llama3decint8", "tinyllama", "tinyllamaprefill"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -429,6 +466,8 @@ def main():
             r = bench_tinyllama_decode(args.steps)
         elif args.leg == "tinyllamaprefill":
             r = bench_tinyllama_prefill(args.steps)
+        elif args.leg == "kvio":
+            r = bench_kv_io(max(1, args.steps))
         elif args.leg.startswith("llama3"):
             r = bench_llama3_mixed(args.steps, int8=args.leg.endswith("int8"),
                                    chunk=0 if args.leg.startswith("llama3dec") else 512)
@@ -454,6 +493,9 @@ def main():
         tp = bench_tinyllama_prefill(5)
         log(f"tinyllama 2048-token prefill forward: {tp}")
         extra["tinyllama_prefill_2048"] = tp
+        kv = bench_kv_io(5)
+        log(f"KV layer I/O (Llama-3-8B layer, 8192 positions): {kv}")
+        extra["kv_layer_io_llama3_8192"] = kv
         c1 = bench_config1()
         log(f"config 1 (SmolLM2 512 + 128 greedy): {c1}")
         extra["smollm2_512_plus_128_greedy"] = c1

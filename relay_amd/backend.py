@@ -136,8 +136,14 @@ class HipBackend:
         _lib.check(_lib.lib().relay_hip_backend_write_kv_block(self._h, layer, block, k.ctypes.data, v.ctypes.data),
                    "write_kv_block")
 
-    def read_kv_layer(self, layer: int, blocks: list) -> np.ndarray:
-        out = np.empty(2 * len(blocks) * self.kv_block_bytes(), np.uint8)
+    def read_kv_layer(self, layer: int, blocks: list, out: np.ndarray | None = None) -> np.ndarray:
+        """All K blocks, then all V blocks (relay's read_kv_layer layout); into `out` (uint8,
+        C-contiguous, the right size) when given, else a new array."""
+        nbytes = 2 * len(blocks) * self.kv_block_bytes()
+        if out is None:
+            out = np.empty(nbytes, np.uint8)
+        elif out.dtype != np.uint8 or out.nbytes != nbytes or not out.flags["C_CONTIGUOUS"]:
+            raise ValueError("read_kv_layer: out must be a C-contiguous uint8 array of 2 * blocks * kv_block_bytes")
         ids = (C.c_int * max(len(blocks), 1))(*blocks)
         _lib.check(_lib.lib().relay_hip_backend_read_kv_layer(self._h, layer, ids, len(blocks), out.ctypes.data),
                    "read_kv_layer")

@@ -133,6 +133,7 @@ class HipBackend final : public Backend {
     if (copy_stream_) (void)hipStreamSynchronize(copy_stream_);
     if (blas_) rocblas_destroy_handle(blas_);
     for (auto e : layer_done_) (void)hipEventDestroy(e);
+    for (auto e : kv_events_) (void)hipEventDestroy(e);
     if (fwd_begin_) (void)hipEventDestroy(fwd_begin_);
     if (fwd_end_) (void)hipEventDestroy(fwd_end_);
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -190,6 +191,9 @@ class HipBackend final : public Backend {
   // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
   static bool skinny(int K, int N, int T);
   void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
+  static constexpr int kKvChunks = 16;                          // pieces of one KV transfer
+  static constexpr std::size_t kKvMinPiece = std::size_t(1) << 20;
+  std::vector<hipEvent_t> kv_events_;                           // one per piece in flight
 
   ModelConfig c_;
   HipOptions opt_;
@@ -582,8 +586,11 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   return out;
 }
 
-// KV block traffic on the copy stream: gather into a contiguous device buffer, one copy
-// to pinned host memory (and the reverse for writes). Serialised by copy_mu_.
+// KV block traffic on the copy stream: gather into a contiguous device buffer and copy it
+// to pinned host memory (and the reverse for writes), in up to kKvChunks pieces so that the
+// host-side memcpy of one piece runs under the DMA of the next (one Llama-3-8B layer at
+// 8192 positions, 33.6 MB, into and out of caller buffers: writes 20.8 -> 30.5 GB/s; reads
+// 26.4 GB/s). Serialised by copy_mu_.
 void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in,
                        const void* v_in) {
   if (layer < 0 || layer >= c_.layers) throw std::invalid_argument("layer out of range");
@@ -601,17 +608,44 @@ void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, v
   std::memcpy(ids, blocks.data(), n * sizeof(int));
   HIP_CHECK(hipMemcpyAsync(kv_ids_dev_.p, ids, n * sizeof(int), hipMemcpyHostToDevice, copy_stream_));
   const std::size_t off = static_cast<std::size_t>(layer) * layout_.layer_elems();
+  if (kv_events_.empty()) {
+    kv_events_.resize(kKvChunks);
+    for (auto& e : kv_events_) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  }
+  // Staging bytes [0, n bb) are K, [n bb, 2 n bb) V; piece i covers [i piece, (i+1) piece).
+  const std::size_t piece = std::max<std::size_t>(kKvMinPiece, (bytes + kKvChunks - 1) / kKvChunks);
+  const int pieces = static_cast<int>((bytes + piece - 1) / piece);
+  auto user_copy = [&](std::size_t a, std::size_t len, bool to_user) {
+    // [a, a + len) of the staging buffer to / from k_out|k_in and v_out|v_in.
+    while (len) {
+      const bool is_k = a < n * bb;
+      const std::size_t rel = is_k ? a : a - n * bb, take = std::min(len, n * bb - rel);
+      auto* u = static_cast<unsigned char*>(is_k ? (to_user ? k_out : const_cast<void*>(k_in))
+                                                 : (to_user ? v_out : const_cast<void*>(v_in)));
+      if (to_user) std::memcpy(u + rel, host + a, take);
+      else std::memcpy(host + a, u + rel, take);
+      a += take;
+      len -= take;
+    }
+  };
   if (k_out) {
     RH_CHECK(rh_kv_gather(kc_.p + off, vc_.p + off, kv_ids_dev_.p, static_cast<int>(n), bb, kv_stage_dev_.p,
                           copy_stream_));
-    HIP_CHECK(hipMemcpyAsync(host, kv_stage_dev_.p, bytes, hipMemcpyDeviceToHost, copy_stream_));
-    HIP_CHECK(hipStreamSynchronize(copy_stream_));
-    std::memcpy(k_out, host, n * bb);
-    std::memcpy(v_out, host + n * bb, n * bb);
+    for (int i = 0; i < pieces; ++i) {
+      const std::size_t a = i * piece, len = std::min(piece, bytes - a);
+      HIP_CHECK(hipMemcpyAsync(host + a, kv_stage_dev_.p + a, len, hipMemcpyDeviceToHost, copy_stream_));
+      HIP_CHECK(hipEventRecord(kv_events_[i], copy_stream_));
+    }
+    for (int i = 0; i < pieces; ++i) {
+      HIP_CHECK(hipEventSynchronize(kv_events_[i]));
+      user_copy(i * piece, std::min(piece, bytes - i * piece), true);
+    }
   } else {
-    std::memcpy(host, k_in, n * bb);
-    std::memcpy(host + n * bb, v_in, n * bb);
-    HIP_CHECK(hipMemcpyAsync(kv_stage_dev_.p, host, bytes, hipMemcpyHostToDevice, copy_stream_));
+    for (int i = 0; i < pieces; ++i) {
+      const std::size_t a = i * piece, len = std::min(piece, bytes - a);
+      user_copy(a, len, false);
+      HIP_CHECK(hipMemcpyAsync(kv_stage_dev_.p + a, host + a, len, hipMemcpyHostToDevice, copy_stream_));
+    }
     RH_CHECK(rh_kv_scatter(kc_.p + off, vc_.p + off, kv_ids_dev_.p, static_cast<int>(n), bb, kv_stage_dev_.p,
                            copy_stream_));
     HIP_CHECK(hipStreamSynchronize(copy_stream_));

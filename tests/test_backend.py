@@ -248,3 +248,18 @@ def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev):
     worst, agree, total = compare(a, b, w.config.vocab, lens, 64, 4)
     print(f"int8 vs fp16, exactly quantizable weights: relative logit difference {worst:.2e}, argmax {agree}/{total}")
     assert worst < 1e-3 and agree >= total - 1
+
+
+def test_read_kv_layer_into_a_caller_buffer(dev):
+    """read_kv_layer into a buffer the caller keeps gives the same bytes as into a new one
+    (relay's KVSender reuses its buffer), and a buffer of the wrong size is refused."""
+    w = small_model(64, 8, 2)
+    be = HipBackend(w, 64, 16, options=FAST)
+    be.fill_kv_random(seed=2, std=1.0)
+    blocks = [5, 0, 63, 17, 17, 40]
+    fresh = be.read_kv_layer(1, blocks)
+    buf = np.full_like(fresh, 0xAB)
+    assert be.read_kv_layer(1, blocks, out=buf) is buf and np.array_equal(buf, fresh)
+    with pytest.raises(ValueError):
+        be.read_kv_layer(1, blocks, out=np.empty(fresh.size - 1, np.uint8))
+    be.close()
