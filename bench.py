@@ -366,9 +366,25 @@ def bench_kv_io(steps=5, ctx=8192):
     be.wait_kv_written(0)
     wr = (time.perf_counter() - t0) / steps
     same = bool(np.array_equal(be.read_kv_layer(0, other), data))
+    # update_weight (relay_engine_update_tensor's path): one down projection, fp32 -> fp16
+    # on the device, from host memory and from a device buffer.
+    import torch
+
+    wd = np.random.default_rng(5).standard_normal((c.hidden, c.intermediate)).astype(np.float32)
+    be.update_weight("layers.1.w_down", wd)
+    t0 = time.perf_counter()
+    be.update_weight("layers.1.w_down", wd)
+    uh = time.perf_counter() - t0
+    wdev = torch.from_numpy(wd).to("cuda:0")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    be.update_weight("layers.1.w_down", wdev)
+    ud = time.perf_counter() - t0
     be.close()
     return {"blocks": n, "bytes": nbytes, "read_ms": round(rd * 1e3, 3), "read_gbs": round(nbytes / rd / 1e9, 1),
-            "write_ms": round(wr * 1e3, 3), "write_gbs": round(nbytes / wr / 1e9, 1), "round_trip_exact": same}
+            "write_ms": round(wr * 1e3, 3), "write_gbs": round(nbytes / wr / 1e9, 1), "round_trip_exact": same,
+            "update_weight_fp32_bytes": wd.nbytes, "update_weight_host_gbs": round(wd.nbytes / uh / 1e9, 1),
+            "update_weight_device_gbs": round(wd.nbytes / ud / 1e9, 1)}
 
 
 # ---- CPU baseline ----------------------------------------------------------------------
