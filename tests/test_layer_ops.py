@@ -33,17 +33,21 @@ def special_floats():
                            rng.standard_normal(100000).astype(np.float32)])
 
 
-def test_f32_to_f16_bit_exact(torch_mod, dev):
+@pytest.mark.parametrize("shift,count", [(0, None), (1, None), (0, 7), (3, 21)])
+def test_f32_to_f16_bit_exact(torch_mod, dev, shift, count):
+    """Aligned (8-wide path plus scalar tail), misaligned (scalar path) and short inputs."""
     from relay_amd import _lib
 
     x = special_floats()
+    n = x.size - shift if count is None else count
     X = torch_mod.from_numpy(x).to(dev)
-    Y = torch_mod.empty(x.size, dtype=torch_mod.int16, device=dev)
-    _lib.check(_lib.lib().rh_f32_to_f16(X.data_ptr(), Y.data_ptr(), x.size, None))
+    Y = torch_mod.full((x.size,), 0x7E00, dtype=torch_mod.int16, device=dev)
+    _lib.check(_lib.lib().rh_f32_to_f16(X.data_ptr() + 4 * shift, Y.data_ptr() + 2 * shift, n, None))
     torch_mod.cuda.synchronize()
     got = Y.cpu().numpy().view(np.uint16)
-    want = O.f32_to_f16(x)
-    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {x.size} differ"
+    want = O.f32_to_f16(x[shift:shift + n])
+    assert np.array_equal(got[shift:shift + n], want), f"{np.count_nonzero(got[shift:shift + n] != want)} of {n} differ"
+    assert (got[:shift] == 0x7E00).all() and (got[shift + n:] == 0x7E00).all()
 
 
 def test_quantize_int8_bit_exact(torch_mod, dev):
