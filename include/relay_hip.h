@@ -249,6 +249,15 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
                 const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
                 int kv_heads, int head_dim, int block_size, void* stream);
 
+/* rh_qkv_post without the fp32 write-back: the same q (fp16, to q_out, required) and cache
+ * rows, qkv left as it is. For callers that read only q_out and the cache afterwards (the
+ * fast attention kernels); saves the fp32 rewrite of every q/k/v value (21 MB per layer for
+ * a 2048-token TinyLlama prefill). No counterpart in relay (qkv_post_kernel rewrites qkv in
+ * place, cuda_backend.cu:171-198). */
+int rh_qkv_post_to_cache(const float* qkv, int T, const float* bias, const float* inv_freq, const int* pos,
+                         const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
+                         void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream);
+
 /* act[t, i] = fp16(g * sigmoid(g) * u), g = gu[t, i], u = gu[t, I + i]. (cuda_backend.cu:245-253) */
 int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream);
 

@@ -76,6 +76,7 @@ SIGNATURES = {
     "rh_embed": (I, [P, I, P, I, P, P]),
     "rh_rmsnorm": (I, [P, P, I, P, I, F, P, P]),
     "rh_qkv_post": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_qkv_post_to_cache": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
     "rh_silu_mul": (I, [P, I, I, P, P]),
     "rh_kv_gather": (I, [P, P, P, I, SZ, P, P]),
     "rh_kv_scatter": (I, [P, P, P, I, SZ, P, P]),

@@ -536,8 +536,13 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
     } else {
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
-      RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads,
-                           c_.kv_heads, D, layout_.block_size, stream_));
+      // The fast kernels read only the fp16 q and the cache; the reference kernel reads qkv.
+      if (q_out)
+        RH_CHECK(rh_qkv_post_to_cache(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out,
+                                      c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+      else
+        RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads,
+                             c_.kv_heads, D, layout_.block_size, stream_));
     }
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
     if (observer) observer->kv_written(l);

@@ -122,6 +122,9 @@ __global__ void rmsnorm_vec_kernel(const float* x, const int* rows, const float*
 // One thread per (token, head, pair (i, i + D/2)) of every head, grid (T, pieces): bias, then
 // RoPE on q and k heads, the fp32 row written back, and the fp16 copies (q to q_out, k and v
 // into the paged cache). Each element is touched by one thread, so no barriers.
+// WRITE_BACK: the rotated fp32 values also go back into qkv (relay's in-place semantics);
+// without it only q (fp16) and the cache rows are written.
+template <bool WRITE_BACK>
 __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_freq, const int* pos, const int* seq,
                                 const int* table_off, const int* tables, half_t* kc, half_t* vc, half_t* q_out,
                                 int heads, int kv_heads, int D, int block_size) {
@@ -147,8 +150,10 @@ __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_
     a = ra;
     b = rb;
   }
-  v[i] = a;
-  v[i + half] = b;
+  if (WRITE_BACK) {
+    v[i] = a;
+    v[i + half] = b;
+  }
   if (h < heads) {
     if (q_out) {
       q_out[static_cast<int64_t>(t) * Q + h * D + i] = static_cast<half_t>(a);
@@ -377,11 +382,26 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
   RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
              "qkv_post: bad shape");
   const int pairs = (heads + 2 * kv_heads) * (head_dim / 2);
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads), 0,
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel<true>, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads), 0,
                                    static_cast<hipStream_t>(stream), qkv,
                                    bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool),
                                    static_cast<half_t*>(vpool), static_cast<half_t*>(q_out), heads, kv_heads,
                                    head_dim, block_size));
+  return 0;
+}
+
+int rh_qkv_post_to_cache(const float* qkv, int T, const float* bias, const float* inv_freq, const int* pos,
+                         const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
+                         void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
+             "qkv_post_to_cache: bad shape");
+  RH_REQUIRE(q_out != nullptr, "qkv_post_to_cache: q_out is required");
+  const int pairs = (heads + 2 * kv_heads) * (head_dim / 2);
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel<false>, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads),
+                                   0, static_cast<hipStream_t>(stream), const_cast<float*>(qkv), bias, inv_freq, pos,
+                                   seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
+                                   static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size));
   return 0;
 }
 

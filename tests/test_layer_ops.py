@@ -254,3 +254,46 @@ def test_silu_mul_within_one_fp16_ulp(torch_mod, dev, T, I):
     got = out.cpu().numpy().view(np.float16)
     ulp = np.abs(np.spacing(want.astype(np.float16)).astype(np.float64))
     assert (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= ulp + 1e-30).all()
+
+
+@pytest.mark.parametrize("bs", [16, 12])
+def test_qkv_post_to_cache_matches_qkv_post(torch_mod, dev, bs):
+    """rh_qkv_post_to_cache writes the same q (fp16) and cache bytes as rh_qkv_post, with
+    real RoPE frequencies and a bias, and leaves qkv as it was."""
+    from relay_amd import _lib
+    from relay_amd.model import tinyllama_1b
+
+    heads, kvh, D = 8, 2, 64
+    Q, KV = heads * D, kvh * D
+    QKV = Q + 2 * KV
+    rng = np.random.default_rng(bs + 7)
+    pos = list(range(30)) + [100, 101, 333]
+    seq = [0] * 30 + [1] * 3
+    nb0, nb1 = (30 + bs - 1) // bs, (334 + bs - 1) // bs
+    nblocks = nb0 + nb1 + 3
+    tables = [int(b) for b in rng.permutation(nblocks)[:nb0 + nb1]]
+    T = len(pos)
+    qkv = rng.standard_normal((T, QKV)).astype(np.float32)
+    inv = O.rope_inv_freq(tinyllama_1b())
+    dt = lambda a: torch_mod.from_numpy(np.ascontiguousarray(a)).to(dev)
+    B, INV = dt(rng.standard_normal(QKV).astype(np.float32)), dt(inv)
+    P, S, TO, TB = dt(np.array(pos, np.int32)), dt(np.array(seq, np.int32)), dt(np.array([0, nb0], np.int32)), \
+        dt(np.array(tables, np.int32))
+    outs = []
+    for fn in ("rh_qkv_post", "rh_qkv_post_to_cache"):
+        X = dt(qkv)
+        kc = torch_mod.full((nblocks * kvh * bs * D,), 0x7BFF, dtype=torch_mod.int16, device=dev)
+        vc = kc.clone()
+        qo = torch_mod.zeros(T * Q, dtype=torch_mod.int16, device=dev)
+        print(f"{fn}: T={T} bs={bs}", flush=True)
+        _lib.check(getattr(_lib.lib(), fn)(X.data_ptr(), T, B.data_ptr(), INV.data_ptr(), P.data_ptr(), S.data_ptr(),
+                                           TO.data_ptr(), TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(),
+                                           heads, kvh, D, bs, None), fn)
+        torch_mod.cuda.synchronize()
+        outs.append([a.cpu().numpy() for a in (X, kc, vc, qo)])
+    (x0, k0, v0, q0), (x1, k1, v1, q1) = outs
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1) and np.array_equal(q0, q1)
+    assert np.array_equal(x1, qkv) and not np.array_equal(x0, qkv)
+    assert _lib.lib().rh_qkv_post_to_cache(None, 1, None, None, None, None, None, None, None, None, None, 8, 2, 64, 16,
+                                           None) != 0
+    assert "q_out is required" in _lib.last_error()
