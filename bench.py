@@ -5,8 +5,10 @@
 
 Prints ONE JSON line. Headline: paged split-context decode
 attention with the fused log-sum-exp merge, 32 sequences x 2048 context, 32 query / 4 KV
-heads, head_dim 64, block size 16, 512-key slices, fp16 Q/K/V ~ N(0, 1), block tables a
-seeded random permutation of the pool. value = algorithmic bytes per launch
+heads, head_dim 64, block size 16, 512-key slices (the config's own split; the slice size
+the host planner picks for this shape, rh_decode_slice_keys, is timed beside it as
+`decode_attention_planner`), fp16 Q/K/V ~ N(0, 1), block tables a seeded random
+permutation of the pool. value = algorithmic bytes per launch
 (K + V + Q + O + tables = 67,387,392 B) / average launch time, with inputs resident in
 HBM; the K steps rotate over enough pool copies (> 256 MB) that the 256 MB Infinity
 Cache cannot hold the working set between launches.
@@ -82,7 +84,7 @@ def decode_case(seed, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16):
 
 
 def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32, kvh=4, D=64, bs=16,
-                 slice_keys=None):
+                 slice_keys=None, table_per_copy=True):
     from relay_amd import _lib
 
     L = _lib.lib()
@@ -97,7 +99,8 @@ def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32
         v = torch.empty_like(k)
         _lib.check(L.rh_fill_normal_f16(k.data_ptr(), k.numel(), 1234, 2 * c, 0.0, 1.0, None))
         _lib.check(L.rh_fill_normal_f16(v.data_ptr(), v.numel(), 1234, 2 * c + 1, 0.0, 1.0, None))
-        tab = torch.from_numpy(np.random.default_rng(c).permutation(nblocks).astype(np.int32)).to(dev)
+        if table_per_copy or c == 0:
+            tab = torch.from_numpy(np.random.default_rng(c).permutation(nblocks).astype(np.int32)).to(dev)
         pools.append((k, v, tab))
     q = torch.empty(n_seq * heads * D, dtype=torch.float16, device=dev)
     _lib.check(L.rh_fill_normal_f16(q.data_ptr(), q.numel(), 1234, 999, 0.0, 1.0, None))
@@ -118,8 +121,8 @@ def bench_decode(torch, dev, stream, steps, warmup, n_seq=32, ctx=2048, heads=32
         k, v, tab = pools[i % copies]
         rc = L.rh_paged_decode_attention(q.data_ptr(), heads * D, k.data_ptr(), v.data_ptr(), dec.data_ptr(),
                                          tab.data_ptr(), n_seq, heads, kvh, D, bs, slice_keys, parts,
-                                         1.0 / math.sqrt(D), part_o.data_ptr(),
-                                         part_ml.data_ptr(), counters.data_ptr(), out.data_ptr(), heads * D, sp)
+                                         1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(),
+                                         counters.data_ptr(), out.data_ptr(), heads * D, sp)
         if rc:
             raise RuntimeError(_lib.last_error())
 
@@ -441,6 +444,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--slice-keys", type=int, default=512,
+                    help="keys per split of the headline decode launch (config 2 specifies 512; 0 = the planner's)")
     ap.add_argument("--leg", choices=["prefill", "prefill128", "kvio", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
                                            "llama3decint8", "tinyllama", "tinyllamaprefill"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
@@ -490,9 +495,14 @@ def main():
         print(json.dumps({"leg": args.leg, **r}), flush=True)
         return
 
-    dec = bench_decode(torch, dev, stream, args.steps, args.warmup)
-    log(f"decode attention: {dec['ms'] * 1e3:.2f} us/launch, {dec['gbs']:.0f} GB/s")
+    dec = bench_decode(torch, dev, stream, args.steps, args.warmup, slice_keys=args.slice_keys or None)
+    log(f"decode attention ({dec['slice_keys']}-key slices): {dec['ms'] * 1e3:.2f} us/launch, {dec['gbs']:.0f} GB/s")
     extra = {}
+    plan = bench_decode(torch, dev, stream, args.steps, args.warmup)
+    log(f"decode attention (planner, {plan['slice_keys']}-key slices): {plan['ms'] * 1e3:.2f} us/launch, "
+        f"{plan['gbs']:.0f} GB/s")
+    extra["decode_attention_planner"] = {"slice_keys": plan["slice_keys"], "us": round(plan["ms"] * 1e3, 2),
+                                         "gbs": round(plan["gbs"], 1), "frac": round(plan["gbs"] / HBM_PEAK_GBS, 4)}
     if not args.quick:
         pre = bench_prefill(torch, dev, stream, 50, 20)  # enough warmup for the clocks to settle
         log(f"prefill attention: {pre['ms'] * 1e3:.1f} us, {pre['tflops']:.1f} TFLOP/s")
