@@ -74,6 +74,21 @@ int rh_paged_decode_attention(const void* q, int64_t q_row_stride, const void* k
                               float* part_o, float* part_ml, int* counters, void* out, int64_t out_row_stride,
                               void* stream);
 
+/* rh_paged_decode_attention without caller scratch, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in relay. The slice partials and arrival counters live in a
+ * static device array of rh_decode_noalloc_scratch_bytes() (16 MiB), held on each GPU the
+ * library runs on until the process ends; the call allocates nothing. Limits:
+ * n_dec * kv_heads * ceil(group / 16) <= 16384 and
+ * 4 * (16384 + n_dec * heads * max_parts * (head_dim + 2)) <= 16 MiB, else an error.
+ * Every call on a GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (different streams, threads or processes' graphs) race and must not be made. */
+int rh_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
+                                      const int* dec_meta, const int* tables, int n_dec, int heads, int kv_heads,
+                                      int head_dim, int block_size, int slice_keys, int max_parts, float scale,
+                                      void* out, int64_t out_row_stride, void* stream);
+size_t rh_decode_noalloc_scratch_bytes(void);
+
 /* Keys per streaming stage of a wave (16 KB of K+V): 64 at head_dim 64, 32 at 128; -1 otherwise. */
 int rh_decode_chunk_keys(int head_dim);
 

@@ -49,6 +49,8 @@ SIGNATURES = {
     "rh_last_error": (C.c_char_p, []),
     "rh_device_available": (I, []),
     "rh_paged_decode_attention": (I, [P, I64, P, P, P, P, I, I, I, I, I, I, I, F, P, P, P, P, I64, P]),
+    "rh_paged_decode_attention_noalloc": (I, [P, I64, P, P, P, P, I, I, I, I, I, I, I, F, P, I64, P]),
+    "rh_decode_noalloc_scratch_bytes": (SZ, []),
     "rh_decode_chunk_keys": (I, [I]),
     "rh_decode_slice_keys": (I, [I, I, I, I, I]),
     "rh_flash_prefill": (I, [P, I64, P, P, P, P, I, I, I, I, I, F, P, I64, P]),

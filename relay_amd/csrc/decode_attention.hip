@@ -37,6 +37,8 @@
 // unnormalized O. Workgroup ids are mapped so the slices of one group land on one XCD
 // (ids are dealt round-robin over the 8 XCDs).
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "../../include/relay_hip.h"
 #include "common.h"
@@ -453,4 +455,82 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
   const bool eight = slice_keys / chunk >= 16;
   if (head_dim == 64) return eight ? launch<64, 8>(a, grid, s) : launch<64, 4>(a, grid, s);
   return eight ? launch<128, 8>(a, grid, s) : launch<128, 4>(a, grid, s);
+}
+
+// ---- the variant that allocates nothing ------------------------------------------------
+//
+// Slice partials and arrival counters in one file-scope device array instead of caller
+// buffers. Layout (floats/ints of 4 bytes): [kNoAllocCounters counters][part_ml][part_o];
+// the counters keep a fixed place so that they stay zero between calls of any shape.
+namespace relay_hip {
+namespace {
+
+constexpr size_t kNoAllocBytes = size_t(16) << 20;     // 16 MiB per device
+constexpr int kNoAllocCounters = 16384;                // (token, kv head, head chunk) groups
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+__global__ void zero_words_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up (and its counters
+// cleared, by a kernel so that the call may sit inside a captured graph) on the first call
+// on each device.
+int noalloc_scratch(hipStream_t s, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string("decode attention (no-alloc): hipGetDevice: ") + hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  RH_REQUIRE(dev >= 0 && dev < kMaxDevices, "decode attention (no-alloc): device index out of range");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(std::string("decode attention (no-alloc): hipGetSymbolAddress: ") + hipGetErrorString(e));
+      return e != hipSuccess ? static_cast<int>(e) : -1;
+    }
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, s, static_cast<int*>(p),
+                                     kNoAllocCounters));
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = g_noalloc_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace relay_hip
+
+extern "C" size_t rh_decode_noalloc_scratch_bytes(void) { return kNoAllocBytes; }
+
+extern "C" int rh_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const void* kpool,
+                                                 const void* vpool, const int* dec_meta, const int* tables, int n_dec,
+                                                 int heads, int kv_heads, int head_dim, int block_size, int slice_keys,
+                                                 int max_parts, float scale, void* out, int64_t out_row_stride,
+                                                 void* stream) {
+  if (n_dec == 0) return 0;
+  RH_REQUIRE(n_dec > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0 && max_parts >= 1,
+             "decode attention (no-alloc): bad sizes");
+  const size_t groups = static_cast<size_t>(n_dec) * kv_heads * ((heads / kv_heads + 15) / 16);
+  const size_t partials = static_cast<size_t>(n_dec) * heads * max_parts;
+  const size_t words = kNoAllocCounters + partials * 2 + partials * static_cast<size_t>(head_dim);
+  RH_REQUIRE(groups <= static_cast<size_t>(kNoAllocCounters) && words * 4 <= kNoAllocBytes,
+             "decode attention (no-alloc): n_dec * heads * max_parts * (head_dim + 2) exceeds the static scratch "
+             "(rh_decode_noalloc_scratch_bytes); use rh_paged_decode_attention with caller buffers");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* base = nullptr;
+  if (int rc = noalloc_scratch(s, &base)) return rc;
+  int* counters = static_cast<int*>(base);
+  float* part_ml = reinterpret_cast<float*>(counters + kNoAllocCounters);
+  float* part_o = part_ml + partials * 2;
+  return rh_paged_decode_attention(q, q_row_stride, kpool, vpool, dec_meta, tables, n_dec, heads, kv_heads, head_dim,
+                                   block_size, slice_keys, max_parts, scale, part_o, part_ml, counters, out,
+                                   out_row_stride, stream);
 }
