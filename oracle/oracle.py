@@ -68,6 +68,7 @@ def ref_lib() -> C.CDLL:
             "ref_generate": (I, [P, IP, I, I, I, IP, P]),
             "ref_f32_to_f16": (None, [P, P, SZ]),
             "ref_rope_inv_freq": (I, [P, P]),
+            "ref_write_kv_block": (I, [P, I, I, P, P]),
             "ref_weight": (C.c_long, [P, C.c_char_p, P, SZ]),
         }
         for name, (res, args) in sig.items():
@@ -171,6 +172,12 @@ class RefBackend:
         if n < 0:
             raise RuntimeError(ref_lib().ref_last_error().decode())
         return list(toks[:n]), logits[:n]
+
+    def write_kv_block(self, layer: int, block: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        if ref_lib().ref_write_kv_block(self._h, layer, block, k.ctypes.data, v.ctypes.data) != 0:
+            raise RuntimeError(ref_lib().ref_last_error().decode())
 
     def rope_inv_freq(self, half: int) -> np.ndarray:
         out = np.empty(half, np.float32)

@@ -101,6 +101,17 @@ int ref_generate(void* hp, const int* prompt, int n, int max_new, int max_batch_
   }
 }
 
+// Backend::write_kv_block of the reference CPU backend (fp32 blocks, cpu_backend.cpp:79-83).
+int ref_write_kv_block(void* hp, int layer, int block, const float* k, const float* v) {
+  try {
+    static_cast<Handle*>(hp)->be->write_kv_block(layer, block, k, v);
+    return 0;
+  } catch (const std::exception& e) {
+    g_error = e.what();
+    return -1;
+  }
+}
+
 void ref_f32_to_f16(const float* in, std::uint16_t* out, size_t n) {
   for (size_t i = 0; i < n; ++i) out[i] = relay::f32_to_f16(in[i]);
 }

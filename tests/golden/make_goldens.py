@@ -28,7 +28,36 @@ import oracle as O  # noqa: E402
 from relay_amd.model import write_safetensors  # noqa: E402
 
 
+def make_steps(name: str) -> None:
+    """A step golden: the reference CPU backend with the seeded cache, the batches of
+    goldens.run_steps; the committed file holds each row's SHA-256, the chosen tokens and
+    the top-2 margins."""
+    c = G.config_of(name)
+    t = time.time()
+    w = G.weights_for(name)
+    _, total = G.step_layout(name)
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(c.to_hf_json(), f)
+        write_safetensors(os.path.join(d, "model.safetensors"), w.to_hf_tensors())
+        ref = O.RefBackend(d, total, G.BLOCK_SIZE)
+        G.fill_step_kv(name, ref, fp16=False)
+        want = G.run_steps(name, ref)
+        del ref
+    print(f"{name}: reference run {time.time() - t:.1f} s", flush=True)
+    mine = G.run_step_oracle(name, w)
+    same = np.array_equal(mine["tokens"], want["tokens"]) and np.array_equal(mine["rows"].view(np.uint32),
+                                                                             want["rows"].view(np.uint32))
+    print(f"{name}: oracle bit-identical to the reference: {same}", flush=True)
+    if not same:
+        raise SystemExit(f"{name}: the oracle differs from the reference build; not writing the golden")
+    np.savez_compressed(os.path.join(HERE, f"{name}.npz"), tokens=want["tokens"], row_sha256=G.row_sha(want["rows"]),
+                        margins=G.margins(want["rows"]))
+
+
 def make(name: str) -> None:
+    if name in G.STEP_GOLDENS:
+        return make_steps(name)
     c, n, steps = G.GOLDENS[name]
     t = time.time()
     w = G.weights_for(name)
@@ -53,5 +82,5 @@ def make(name: str) -> None:
 if __name__ == "__main__":
     if not O.ref_available():
         raise SystemExit("oracle/_ref is not built (needs /root/reference): make -C oracle ref")
-    for name in sys.argv[1:] or list(G.GOLDENS):
+    for name in sys.argv[1:] or list(G.GOLDENS) + list(G.STEP_GOLDENS):
         make(name)

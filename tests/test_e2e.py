@@ -1,6 +1,9 @@
 """End-to-end parity of the HIP backend with the CPU oracle on the whole-model goldens
 (tests/goldens.py): BASELINE config 1 (SmolLM2-135M shape, 512-token prompt, 128 greedy
-steps) and 2-layer variants of configs 3 and 5.
+steps), 2-layer variants of configs 3 and 5, config 3(a)'s 2048-token prompt in one chunk,
+and step goldens at the configs' batch shapes: config 3(b)'s decode step of 32 sequences at
+context 2048 and config 5's mixed step (48 decode sequences plus a 512-token chunk in one
+ForwardBatch), each followed by one more step.
 
 The oracle (the fp32 CPU restatement, bit-identical to the reference build's CPU backend
 on these goldens, test_oracle.py) runs on the same synthetic weights. The bar
@@ -18,7 +21,7 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.mark.parametrize("name", ["smollm2_135m", "tinyllama_2layer", "llama3_8b_2layer"])
+@pytest.mark.parametrize("name", ["smollm2_135m", "tinyllama_2layer", "llama3_8b_2layer", "tinyllama_2layer_p2048"])
 def test_greedy_run_matches_the_oracle(dev, name):
     import os
 
@@ -39,3 +42,34 @@ def test_greedy_run_matches_the_oracle(dev, name):
           f"smallest top-2 margin {float(golden['margins'].min()):.3e}", flush=True)
     assert got["tokens"].tolist() == golden["tokens"].tolist()
     assert max(errs) <= TOL
+
+
+@pytest.mark.parametrize("name", ["tinyllama_2layer_decode32", "llama3_8b_2layer_mixed"])
+def test_step_matches_the_oracle(dev, name):
+    """Both backends get the same seeded cache and the same inputs (step 2 feeds the golden's
+    step-1 tokens). Every row within 2e-3 of the oracle's; every greedy token equal to the
+    golden's wherever the golden's top-2 margin exceeds what the tolerance allows, i.e.
+    2 * 2e-3 * max|row| (near-ties of synthetic weights are reported, not asserted)."""
+    import os
+
+    from relay_amd.backend import HipBackend, HipOptions
+
+    golden = np.load(os.path.join(os.path.dirname(__file__), "golden", f"{name}.npz"), allow_pickle=False)
+    w = G.weights_for(name)
+    print(f"step {name}: oracle run", flush=True)
+    want = G.run_step_oracle(name, w)
+    assert np.array_equal(want["tokens"], golden["tokens"])
+    print(f"step {name}: HIP run", flush=True)
+    _, total = G.step_layout(name)
+    be = HipBackend(w, total, G.BLOCK_SIZE, max_batch_tokens=G.MAX_BATCH_TOKENS, options=HipOptions(False, False))
+    G.fill_step_kv(name, be, fp16=True)
+    got = G.run_steps(name, be, forced=golden["tokens"])
+    be.close()
+    errs = [rel_err_rowmax(a, b) for a, b in zip(got["rows"], want["rows"])]
+    rowmax = np.abs(want["rows"]).max(axis=1)
+    decisive = golden["margins"] > 2 * TOL * rowmax
+    flips = int(((got["tokens"].ravel() != golden["tokens"].ravel()) & ~decisive).sum())
+    print(f"step {name}: rows {len(errs)}, worst rel err {max(errs):.2e}, decisive rows {int(decisive.sum())}, "
+          f"near-tie flips {flips}", flush=True)
+    assert max(errs) <= TOL
+    assert np.array_equal(got["tokens"].ravel()[decisive], golden["tokens"].ravel()[decisive])

@@ -226,7 +226,7 @@ def test_gemv_oracle_is_exact_on_a_small_case():
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
-@pytest.mark.parametrize("name", ["smollm2_135m", "tinyllama_2layer", "llama3_8b_2layer"])
+@pytest.mark.parametrize("name", ["smollm2_135m", "tinyllama_2layer", "llama3_8b_2layer", "tinyllama_2layer_p2048"])
 def test_oracle_equals_committed_goldens(name):
     """Goldens written by tests/golden/make_goldens.py from the reference build: the same
     greedy tokens and every logits row bit for bit (by SHA-256)."""
@@ -237,4 +237,17 @@ def test_oracle_equals_committed_goldens(name):
     assert g["prompt"].tolist() == goldens.prompt_of(name)
     got = goldens.run_oracle(name, goldens.weights_for(name))
     assert got["tokens"].tolist() == g["tokens"].tolist()
+    assert np.array_equal(goldens.row_sha(got["rows"]), g["row_sha256"])
+
+
+@pytest.mark.parametrize("name", ["tinyllama_2layer_decode32", "llama3_8b_2layer_mixed"])
+def test_oracle_equals_committed_step_goldens(name):
+    """Step goldens (a 32-sequence decode step at context 2048; a mixed step of 48 decode
+    sequences and a 512-token chunk), written from the reference build by
+    tests/golden/make_goldens.py: every logits row bit for bit and the same greedy tokens."""
+    import goldens
+
+    g = np.load(os.path.join(GOLDEN, f"{name}.npz"), allow_pickle=False)
+    got = goldens.run_step_oracle(name, goldens.weights_for(name))
+    assert np.array_equal(got["tokens"], g["tokens"])
     assert np.array_equal(goldens.row_sha(got["rows"]), g["row_sha256"])
