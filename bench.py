@@ -422,6 +422,81 @@ def cpu_baseline(sample_seqs=8, ctx=2048, heads=32, kvh=4, D=64, bs=16):
                       f"{per_call * 1e3:.1f} ms each"}
 
 
+def host_cpu():
+    """This host's core count (as the OpenMP oracle uses them) and CPU model name (lscpu)."""
+    import subprocess
+
+    model = ""
+    try:
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001 - lscpu missing: report no name
+        pass
+    return {"nproc": os.cpu_count(), "omp_threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+            "model": model}
+
+
+def cpu_config1(prompt_len=512, new_tokens=128):
+    """Config 1 end to end on the CPU oracle (relay's fp32 CPU backend, OpenMP on this host's
+    cores): SmolLM2-135M shape, synthetic fp32 weights, 512-token prompt + 128 greedy steps
+    through relay's batch composition."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    from relay_amd import smollm2_135m
+    from relay_amd.engine import GreedyEngine
+    from relay_amd.model import HostWeights
+
+    c = smollm2_135m()
+    bs = 16
+    nb = (prompt_len + new_tokens) // bs + 2
+    w = HostWeights.synthetic(c, seed=0)
+    cpu = O.CpuBackend(w, nb, bs)
+    prompt = np.random.default_rng(0).integers(0, c.vocab, size=prompt_len).tolist()
+    marks = []
+    eng = GreedyEngine(cpu, nb, bs, 2048, 8, on_logits=lambda rid, i, row: marks.append(time.perf_counter()))
+    eng.add(1, prompt, new_tokens)
+    t0 = time.perf_counter()
+    out = eng.run_all()[1]
+    t1 = time.perf_counter()
+    assert len(out) == new_tokens
+    return {"prompt_s": round(marks[0] - t0, 3), "decode_tok_s": round((new_tokens - 1) / (t1 - marks[0]), 2),
+            "total_s": round(t1 - t0, 3), "gen_tok_s": round(new_tokens / (t1 - t0), 2)}
+
+
+def cpu_tinyllama_decode(n_seq=32, ctx=2048, layers=22):
+    """Config 3(b) on the CPU oracle: one decode step of n_seq sequences at context ctx
+    through all `layers` TinyLlama layers (synthetic fp32 weights); the step alone is timed.
+    The cache is left as constructed (zeros): the oracle's work does not depend on the
+    values, and writing 2.9 GB of fp32 blocks through the per-block call would take longer
+    than the step."""
+    import dataclasses
+
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    from relay_amd import tinyllama_1b
+    from relay_amd.backend import ForwardBatch, SeqChunk
+    from relay_amd.model import HostWeights
+
+    c = dataclasses.replace(tinyllama_1b(), layers=layers)
+    bs = 16
+    per = ctx // bs + 1
+    w = HostWeights.synthetic(c, seed=0)
+    cpu = O.CpuBackend(w, n_seq * per, bs)
+    rng = np.random.default_rng(3)
+    batch = ForwardBatch([SeqChunk([int(rng.integers(c.vocab))], ctx - 1, list(range(i * per, (i + 1) * per)), True)
+                          for i in range(n_seq)])
+    times = []
+    for _ in range(2):  # the same step twice (it rewrites the same cache slots); the faster counts
+        t0 = time.perf_counter()
+        cpu.forward(batch)
+        times.append((time.perf_counter() - t0) * 1e3)
+    ms = min(times)
+    return {"layers": layers, "ms": round(ms, 1), "tok_s": round(n_seq / ms * 1e3, 2)}
+
+
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_attention_config2_traffic.md")
 
 
@@ -529,7 +604,18 @@ def main():
             l3 = bench_llama3_mixed(5, int8=int8)
             log(f"llama3-8b mixed step (48 x 8192 decode + 512 chunk){' int8' if int8 else ''}: {l3}")
             extra["llama3_8b_mixed_step" + ("_int8" if int8 else "")] = l3
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+        cpu["host"] = host_cpu()
+        log(f"cpu baseline (attention): {cpu}")
+        if not args.quick:
+            c1 = cpu_config1()
+            log(f"cpu config 1: {c1}")
+            td = cpu_tinyllama_decode()
+            log(f"cpu tinyllama 32 x 2048 decode step: {td}")
+            cpu["config1_smollm2_512_plus_128"] = c1
+            cpu["tinyllama_decode_32x2048"] = td
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 1),
