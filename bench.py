@@ -261,6 +261,50 @@ def bench_tinyllama_prefill(steps, S=2048):
             "tflops_device": round((gemm_flops + attn_flops) / dev_ms / 1e9, 1)}
 
 
+def bench_prefill_chunked(steps, length, int8=False, chunk=512):
+    """A length-token TinyLlama prompt in chunk-token chunks, one forward per chunk, as
+    relay's attention bench times it (tools/relay_attention_bench.cpp:37-60); wall ms of the
+    whole prompt (host included) and device ms summed over the chunks."""
+    from relay_amd import HipBackend, HipOptions, tinyllama_1b
+    from relay_amd.backend import ForwardBatch, SeqChunk
+
+    c = tinyllama_1b()
+    bs = 16
+    nb = (length + bs - 1) // bs + 1
+    be = HipBackend(None, nb, bs, max_batch_tokens=chunk, max_context=nb * bs, options=HipOptions(False, int8),
+                    config=c, synthetic_seed=0, synthetic_std=0.02)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, c.vocab, size=length).tolist()
+    walls, devs = [], []
+    for r in range(steps + 1):  # the first run warms up
+        t0 = time.perf_counter()
+        dev = 0.0
+        for s0 in range(0, length, chunk):
+            be.forward(ForwardBatch([SeqChunk(prompt[s0:s0 + chunk], s0, list(range(nb)), True)]))
+            dev += be.last_forward_ms()
+        if r:
+            walls.append((time.perf_counter() - t0) * 1e3)
+            devs.append(dev)
+    be.close()
+    return {"ms_wall": round(float(np.median(walls)), 3), "ms_device": round(float(np.median(devs)), 3)}
+
+
+def bench_reference_points(steps=5):
+    """The measurement points relay publishes for TinyLlama-1.1B (results/t4/m1-2026-10-04.txt:
+    51-59): prefill of 512 and 2048 tokens in 512-token chunks, and decode steps at batch 1, 8
+    and 32 and context 512 and 2048, each with fp16 and with int8 weights."""
+    out = {}
+    for int8 in (False, True):
+        tag = "int8" if int8 else "fp16"
+        for n in (512, 2048):
+            out[f"prefill_{n}_{tag}"] = bench_prefill_chunked(steps, n, int8)
+        for ctx in (512, 2048):
+            for b in (1, 8, 32):
+                r = bench_tinyllama_decode(steps, int8=int8, n_seq=b, ctx=ctx)
+                out[f"decode_b{b}_ctx{ctx}_{tag}"] = r
+    return out
+
+
 # ---- config 1: SmolLM2-135M, 512-token prompt + 128 greedy steps --------------------------
 
 def bench_config1(prompt_len=512, new_tokens=128):
@@ -522,8 +566,11 @@ def main():
     ap.add_argument("--slice-keys", type=int, default=512,
                     help="keys per split of the headline decode launch (config 2 specifies 512; 0 = the planner's)")
     ap.add_argument("--leg", choices=["prefill", "prefill128", "kvio", "gemv", "config1", "llama3", "llama3int8", "llama3dec",
-                                           "llama3decint8", "tinyllama", "tinyllamaprefill"],
+                                           "llama3decint8", "tinyllama", "tinyllamaprefill", "refpoints"],
                     help="run only this part (for profiling) and print its numbers as one JSON line")
+    ap.add_argument("--nseq", type=int, default=32, help="--leg tinyllama: decode batch")
+    ap.add_argument("--ctx", type=int, default=2048, help="--leg tinyllama: context")
+    ap.add_argument("--int8", action="store_true", help="--leg tinyllama: int8 weights")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters under rocprofv3 --pmc)")
@@ -559,7 +606,9 @@ def main():
         elif args.leg == "config1":
             r = bench_config1()
         elif args.leg == "tinyllama":
-            r = bench_tinyllama_decode(args.steps)
+            r = bench_tinyllama_decode(args.steps, int8=args.int8, n_seq=args.nseq, ctx=args.ctx)
+        elif args.leg == "refpoints":
+            r = bench_reference_points(max(1, min(args.steps, 10)))
         elif args.leg == "tinyllamaprefill":
             r = bench_tinyllama_prefill(args.steps)
         elif args.leg == "kvio":
@@ -591,6 +640,9 @@ def main():
         extra["tinyllama_decode_32x2048"] = td
         td8 = bench_tinyllama_decode(10, int8=True)
         extra["tinyllama_decode_32x2048_int8"] = td8
+        rp = bench_reference_points(5)
+        log(f"relay's TinyLlama measurement points: {rp}")
+        extra["tinyllama_reference_points"] = rp
         tp = bench_tinyllama_prefill(5)
         log(f"tinyllama 2048-token prefill forward: {tp}")
         extra["tinyllama_prefill_2048"] = tp

@@ -67,7 +67,8 @@ int rh_device_available(void);
  *              before the first call; every call leaves them zero again. Calls that share
  *              counters must not overlap in time (same stream is fine)
  *  scale       softmax scale (1/sqrt(head_dim) in relay)
- * head_dim in {64, 128}; any group size (query heads are processed 16 at a time). */
+ * head_dim in {16, 32, 64, 128} (16 computed at width 32); any group size (query heads are
+ * processed 16 at a time). */
 int rh_paged_decode_attention(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool,
                               const int* dec_meta, const int* tables, int n_dec, int heads, int kv_heads,
                               int head_dim, int block_size, int slice_keys, int max_parts, float scale,
@@ -89,7 +90,8 @@ int rh_paged_decode_attention_noalloc(const void* q, int64_t q_row_stride, const
                                       void* out, int64_t out_row_stride, void* stream);
 size_t rh_decode_noalloc_scratch_bytes(void);
 
-/* Keys per streaming stage of a wave (16 KB of K+V): 64 at head_dim 64, 32 at 128; -1 otherwise. */
+/* Keys per streaming stage of a wave (16 KB of K+V at head_dim 64 and 128, 8 KB at 32): 128 at
+ * head_dim 16 and 32, 64 at 64, 32 at 128; -1 otherwise. */
 int rh_decode_chunk_keys(int head_dim);
 
 /* The slice_keys rh_paged_decode_attention runs fastest with on MI355X for a step of n_dec
@@ -106,7 +108,7 @@ int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int m
  *              two blocks of rows (first row, rows, first position) and the chunk's
  *              block-table offset
  *  tables      the block tables the records' offsets point into
- * head_dim in {64, 128}. */
+ * head_dim in {16, 32, 64, 128} (16 computed at width 32). */
 int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool, const int* tables,
                      const int* work, int n_work, int heads, int kv_heads, int head_dim, int block_size, float scale,
                      void* out, int64_t out_row_stride, void* stream);

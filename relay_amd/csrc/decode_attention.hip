@@ -67,12 +67,17 @@ struct DecodeArgs {
 // Slices merged with all their loads issued together (more take a plain loop).
 constexpr int kMergeBatch = 8;
 
-// Swizzle of a key's 16-byte chunks in the V staging rows.
-__device__ __forceinline__ int vswz(int key) { return ((key >> 2) & 3) << 1; }
+// Swizzle of a key's 16-byte chunks in the V staging rows (within the row's D / 8 chunks).
+template <int D>
+__device__ __forceinline__ int vswz(int key) {
+  return D >= 64 ? ((key >> 2) & 3) << 1 : ((key >> 2) & 1) << 1;
+}
 
+// Keys per streaming stage of a wave: 16 KB of K+V at head sizes 64 and 128, 8 KB at 32
+// (also the compute width of head size 16).
 template <int D>
 constexpr int stage_keys() {
-  return D == 64 ? 64 : 32;
+  return D == 64 ? 64 : D == 128 ? 32 : 128;
 }
 
 // One chunk of a wave's K and V in registers.
@@ -86,7 +91,9 @@ struct Stage {
 };
 
 // SCALAR: block_size is a power of two >= 16 (table entries are wave-uniform per tile).
-template <int D, int WAVES, bool SCALAR>
+// D is the compute width, DR the head size of the cache rows, q and out: equal, except head
+// size 16, which runs at width 32 with dims 16..31 of K, V and q taken as zero.
+template <int D, int DR, int WAVES, bool SCALAR>
 __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_decode_kernel(
     const DecodeArgs a) {
   constexpr int SK = stage_keys<D>();
@@ -98,6 +105,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
   constexpr int VKEYS = kWave / CH;                 // keys covered by one V load
   constexpr int NT = WAVES * kWave;
   static_assert(kStepKeys * D * 2 == 16 * D * 4, "the merge area reuses the V staging");
+  static_assert(DR == D || (DR == 16 && D == 32), "head size 16 runs at width 32");
 
   __shared__ __attribute__((aligned(16))) half_t s_v[WAVES][kStepKeys * D];
   __shared__ float s_m[WAVES][16], s_l[WAVES][16];
@@ -163,10 +171,20 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int h = 0; h < KH; ++h)
-          st.k[s][tt][h] = load_half8(a.kpool + static_cast<int64_t>(krow[s][tt]) * D + 32 * h + 8 * g);
+          if (DR == D || 32 * h + 8 * g < DR) {
+            st.k[s][tt][h] = load_half8(a.kpool + static_cast<int64_t>(krow[s][tt]) * DR + 32 * h + 8 * g);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) st.k[s][tt][h][e] = 0;
+          }
 #pragma unroll
       for (int i = 0; i < VL; ++i)
-        st.v[s][i] = load_half8(a.vpool + static_cast<int64_t>(vrow[s][i]) * D + 8 * (lane % CH));
+        if (DR == D || 8 * (lane % CH) < DR) {
+          st.v[s][i] = load_half8(a.vpool + static_cast<int64_t>(vrow[s][i]) * DR + 8 * (lane % CH));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) st.v[s][i][e] = 0;
+        }
     }
   };
 
@@ -193,7 +211,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = 0;
         }
-        *reinterpret_cast<half8*>(sv + kl * D + ((cc ^ vswz(kl)) << 3)) = v;
+        *reinterpret_cast<half8*>(sv + kl * D + ((cc ^ vswz<D>(kl)) << 3)) = v;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -240,8 +258,8 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
         // and 16 + 4g give the operand's two runs of 4 keys.
         const int col = 16 * dt + 4 * (c & 3);
         const int k0r = 4 * g + (c >> 2), k1r = 16 + 4 * g + (c >> 2);
-        const half4 lo = tr_read_b64(sv + k0r * D + (((col >> 3) ^ vswz(k0r)) << 3) + (col & 7));
-        const half4 hi = tr_read_b64(sv + k1r * D + (((col >> 3) ^ vswz(k1r)) << 3) + (col & 7));
+        const half4 lo = tr_read_b64(sv + k0r * D + (((col >> 3) ^ vswz<D>(k0r)) << 3) + (col & 7));
+        const half4 hi = tr_read_b64(sv + k1r * D + (((col >> 3) ^ vswz<D>(k1r)) << 3) + (col & 7));
         const half8 vt = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         float4v acc = o[dt];
 #pragma unroll
@@ -262,8 +280,9 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
     if (!have_q) {
 #pragma unroll
       for (int h = 0; h < KH; ++h) {
-        if (c < nh) {
-          qb[h] = load_half8(a.q + static_cast<int64_t>(t) * a.q_stride + static_cast<int64_t>(h0 + c) * D + 32 * h + 8 * g);
+        if (c < nh && (DR == D || 32 * h + 8 * g < DR)) {
+          qb[h] = load_half8(a.q + static_cast<int64_t>(t) * a.q_stride + static_cast<int64_t>(h0 + c) * DR + 32 * h +
+                             8 * g);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) qb[h][e] = 0;
@@ -292,8 +311,8 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
   __syncthreads();
 
   const bool single = nparts == 1;
-  for (int idx = threadIdx.x; idx < nh * D; idx += NT) {
-    const int hh = idx / D, d = idx % D;
+  for (int idx = threadIdx.x; idx < nh * DR; idx += NT) {
+    const int hh = idx / DR, d = idx % DR;
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < WAVES; ++ww) M = fmaxf(M, s_m[ww][hh]);
@@ -308,10 +327,10 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
       }
     }
     if (single) {
-      a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * D + d] = static_cast<half_t>(O / L);
+      a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * DR + d] = static_cast<half_t>(O / L);
     } else {
       const int64_t pb = (static_cast<int64_t>(di) * a.heads + h0 + hh) * a.max_parts + part;
-      coherent_store(&a.part_o[pb * D + d], O);
+      coherent_store(&a.part_o[pb * DR + d], O);
       if (d == 0) {
         coherent_store(&a.part_ml[pb * 2], M);
         coherent_store(&a.part_ml[pb * 2 + 1], L);
@@ -333,8 +352,8 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
   }
   __syncthreads();
   if (!s_last) return;
-  for (int idx = threadIdx.x; idx < nh * D; idx += NT) {
-    const int hh = idx / D, d = idx % D;
+  for (int idx = threadIdx.x; idx < nh * DR; idx += NT) {
+    const int hh = idx / DR, d = idx % DR;
     const int64_t base = (static_cast<int64_t>(di) * a.heads + h0 + hh) * a.max_parts;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
     if (nparts <= kMergeBatch) {
@@ -346,7 +365,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
         if (p < nparts) {
           mv[p] = coherent_load(&a.part_ml[(base + p) * 2]);
           lv[p] = coherent_load(&a.part_ml[(base + p) * 2 + 1]);
-          ov[p] = coherent_load(&a.part_o[(base + p) * D + d]);
+          ov[p] = coherent_load(&a.part_o[(base + p) * DR + d]);
         }
       }
 #pragma unroll
@@ -365,21 +384,28 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
       for (int p = 0; p < nparts; ++p) {
         const float f = fast_exp2(coherent_load(&a.part_ml[(base + p) * 2]) - M);
         L += f * coherent_load(&a.part_ml[(base + p) * 2 + 1]);
-        O += f * coherent_load(&a.part_o[(base + p) * D + d]);
+        O += f * coherent_load(&a.part_o[(base + p) * DR + d]);
       }
     }
-    a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * D + d] = static_cast<half_t>(O / L);
+    a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * DR + d] = static_cast<half_t>(O / L);
   }
 }
 
-template <int D, int WAVES>
+template <int D, int DR, int WAVES>
 int launch(const DecodeArgs& a, int grid, hipStream_t s) {
   if (a.bs_shift >= 4) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<D, WAVES, true>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
+    RH_TRY_LAUNCH(
+        hipLaunchKernelGGL((paged_decode_kernel<D, DR, WAVES, true>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((paged_decode_kernel<D, WAVES, false>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
+    RH_TRY_LAUNCH(
+        hipLaunchKernelGGL((paged_decode_kernel<D, DR, WAVES, false>), dim3(grid), dim3(WAVES * kWave), 0, s, a));
   }
   return 0;
+}
+
+template <int D, int DR>
+int launch_waves(const DecodeArgs& a, int grid, bool eight, hipStream_t s) {
+  return eight ? launch<D, DR, 8>(a, grid, s) : launch<D, DR, 4>(a, grid, s);
 }
 
 }  // namespace
@@ -388,17 +414,28 @@ int launch(const DecodeArgs& a, int grid, hipStream_t s) {
 using namespace relay_hip;
 
 extern "C" int rh_decode_chunk_keys(int head_dim) {
-  return head_dim == 64 ? stage_keys<64>() : head_dim == 128 ? stage_keys<128>() : -1;
+  switch (head_dim) {
+    case 16:
+    case 32: return stage_keys<32>();
+    case 64: return stage_keys<64>();
+    case 128: return stage_keys<128>();
+    default: return -1;
+  }
 }
 
 extern "C" int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int max_ctx) {
   const int chunk = rh_decode_chunk_keys(head_dim);
   if (chunk <= 0 || n_dec <= 0 || max_ctx <= 0) return chunk;
-  // Measured on MI355X (1 x 640 / D64 up to 48 x 8192 / D128): one slice for at most 16
+  // Measured on MI355X (1 x 640 / D64 up to 48 x 8192 / D128), otherwise: one slice for at most 16
   // (context, kv head) groups of at most 16 chunks; otherwise at least two slices per
   // context (enough workgroups to spread over the 256 CUs), more while there are fewer
   // than 256 groups, but never below 8 chunks (one per wave of an 8-wave workgroup).
   const long groups = static_cast<long>(n_dec) * kv_heads * ((group + 15) / 16);
+  // Head size 64 with few groups: the step is latency-bound, so slices of 4 chunks (one per
+  // wave of a 4-wave workgroup) as long as that makes at most 256 workgroups. Measured:
+  // 1 x 640 keys, 9/3 heads (config 1) 10.2 -> 6.9 us; 1 x 2048, 32/4 11.7 -> 9.0 us;
+  // 8 x 2048, 32/4 12.8 -> 11.1 us. (At head size 128 the same split measured slower.)
+  if (head_dim == 64 && groups * ((max_ctx + 4 * chunk - 1) / (4 * chunk)) <= 256) return 4 * chunk;
   // A handful of short contexts: one slice (no merge); the launch is latency-bound anyway.
   if (groups <= 16 && max_ctx <= 16 * chunk) return (max_ctx + chunk - 1) / chunk * chunk;
   const long parts = std::max(2L, 256 / groups);
@@ -414,7 +451,8 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
                                          int64_t out_row_stride, void* stream) {
   if (n_dec == 0) return 0;
   RH_REQUIRE(n_dec > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "decode attention: bad head counts");
-  RH_REQUIRE(head_dim == 64 || head_dim == 128, "decode attention: head_dim must be 64 or 128");
+  RH_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128,
+             "decode attention: head_dim must be 16, 32, 64 or 128");
   RH_REQUIRE(block_size > 0, "decode attention: bad block size");
   const int chunk = rh_decode_chunk_keys(head_dim);
   RH_REQUIRE(slice_keys >= chunk && slice_keys % chunk == 0,
@@ -453,8 +491,12 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
   // config 2: 512-key slices on 8 waves run their 512 workgroups in two rounds, 24.2 us,
   // against 18.8 us on 4 waves).
   const bool eight = slice_keys / chunk >= 16;
-  if (head_dim == 64) return eight ? launch<64, 8>(a, grid, s) : launch<64, 4>(a, grid, s);
-  return eight ? launch<128, 8>(a, grid, s) : launch<128, 4>(a, grid, s);
+  switch (head_dim) {
+    case 16: return launch_waves<32, 16>(a, grid, eight, s);
+    case 32: return launch_waves<32, 32>(a, grid, eight, s);
+    case 64: return launch_waves<64, 64>(a, grid, eight, s);
+    default: return launch_waves<128, 128>(a, grid, eight, s);
+  }
 }
 
 // ---- the variant that allocates nothing ------------------------------------------------

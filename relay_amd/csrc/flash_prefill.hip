@@ -52,7 +52,7 @@ constexpr int kThreads = kWaves * kWave;
 // one softmax (measured 45.0 -> 41.8 us at config 3); at D 128 the second chain's
 // registers would spill.
 template <int D>
-constexpr int sub_steps() { return D == 64 ? 2 : 1; }
+constexpr int sub_steps() { return D == 128 ? 1 : 2; }
 
 // One work item: block a (t0, rows, first position), block b likewise (rows 0: none), and
 // the chunk's block-table offset. Layout of rh_prefill_plan's int32[8] records.
@@ -77,10 +77,15 @@ struct PrefillArgs {
 // chunks (bank conflicts halved, 56.3 -> 55.0 us at 2048 tokens); at D64 the same change
 // measured slower (32.4 -> 34.0 us), so it keeps key & 7.
 template <int D>
-__device__ __forceinline__ int kswz(int key) { return D == 128 ? (key ^ ((key >> 3) & 3)) & 7 : key & 7; }
+__device__ __forceinline__ int kswz(int key) {
+  return D == 128 ? (key ^ ((key >> 3) & 3)) & 7 : D == 64 ? key & 7 : key & 3;  // within the D / 8 chunks
+}
 
-template <int D, bool POW2>
+// D is the compute width, DR the head size of the cache rows, q and out: equal, except head
+// size 16, which runs at width 32 with dims 16..31 of K, V and q taken as zero.
+template <int D, int DR, bool POW2>
 __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillArgs a) {
+  static_assert(DR == D || (DR == 16 && D == 32), "head size 16 runs at width 32");
   constexpr int kSub = sub_steps<D>();      // 32-key sub-steps per wave per tile
   constexpr int kKeyTile = 64 * kSub;       // keys per LDS tile
   constexpr int CH = D / 8;                                 // 16-byte chunks per row
@@ -160,9 +165,14 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
         if (item(i, kl, cc)) {
           const int key = min(k0 + kl, nkeys - 1);
           const int slot = POW2 ? key & (bs - 1) : key % bs;
-          const int64_t off = kv_row_offset(blk[i], a.kv_heads, kvh, bs, slot, D) + 8 * cc;
-          kreg[i] = load_half8(a.kpool + off);
-          vreg[i] = load_half8(a.vpool + off);
+          const int64_t off = kv_row_offset(blk[i], a.kv_heads, kvh, bs, slot, DR) + 8 * cc;
+          if (DR == D || 8 * cc < DR) {
+            kreg[i] = load_half8(a.kpool + off);
+            vreg[i] = load_half8(a.vpool + off);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kreg[i][e] = vreg[i][e] = 0;
+          }
         }
       }
     };
@@ -185,8 +195,8 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
     half8 qb[MK];
 #pragma unroll
     for (int m = 0; m < MK; ++m) {
-      if (row_ok) {
-        qb[m] = load_half8(a.q + static_cast<int64_t>(t0 + row) * a.q_stride + static_cast<int64_t>(head) * D +
+      if (row_ok && (DR == D || 16 * m + 8 * hh < DR)) {
+        qb[m] = load_half8(a.q + static_cast<int64_t>(t0 + row) * a.q_stride + static_cast<int64_t>(head) * DR +
                            16 * m + 8 * hh);
       } else {
 #pragma unroll
@@ -331,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
       const float fb = m_b == -INFINITY ? 0.0f : fast_exp2((m_b - m) * cl);
       const float l = l_part * fa + l_b * fb;
       const float inv = 1.0f / (l + __shfl_xor(l, 32));
-      half_t* orow = a.out + static_cast<int64_t>(t0 + row) * a.out_stride + static_cast<int64_t>(head) * D;
+      half_t* orow = a.out + static_cast<int64_t>(t0 + row) * a.out_stride + static_cast<int64_t>(head) * DR;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -342,19 +352,19 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
             const int r = 4 * r4 + j;
             v[j] = static_cast<half_t>((o[dt][r] * fa + xo[(dt * 16 + r) * 64 + lane] * fb) * inv);
           }
-          *reinterpret_cast<half4*>(orow + 32 * dt + 8 * r4 + 4 * hh) = v;
+          if (DR == D || 32 * dt + 8 * r4 + 4 * hh < DR) *reinterpret_cast<half4*>(orow + 32 * dt + 8 * r4 + 4 * hh) = v;
         }
     }
   }
 }
 
-template <int D>
+template <int D, int DR>
 int launch(const PrefillArgs& a, hipStream_t s) {
   const int grid = a.n_work * a.heads;
   if (a.bs_shift >= 0) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, true>), dim3(grid), dim3(kThreads), 0, s, a));
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, DR, true>), dim3(grid), dim3(kThreads), 0, s, a));
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, false>), dim3(grid), dim3(kThreads), 0, s, a));
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((flash_prefill_kernel<D, DR, false>), dim3(grid), dim3(kThreads), 0, s, a));
   }
   return 0;
 }
@@ -418,7 +428,8 @@ extern "C" int rh_flash_prefill(const void* q, int64_t q_row_stride, const void*
                                 int block_size, float scale, void* out, int64_t out_row_stride, void* stream) {
   if (n_work == 0) return 0;
   RH_REQUIRE(n_work > 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "flash prefill: bad head counts");
-  RH_REQUIRE(head_dim == 64 || head_dim == 128, "flash prefill: head_dim must be 64 or 128");
+  RH_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128,
+             "flash prefill: head_dim must be 16, 32, 64 or 128");
   RH_REQUIRE(block_size > 0, "flash prefill: bad block size");
   RH_REQUIRE(q_row_stride % 8 == 0 && out_row_stride % 4 == 0, "flash prefill: rows must be aligned");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kpool) |
@@ -442,5 +453,10 @@ extern "C" int rh_flash_prefill(const void* q, int64_t q_row_stride, const void*
   a.out = static_cast<half_t*>(out);
   a.out_stride = out_row_stride;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return head_dim == 64 ? launch<64>(a, s) : launch<128>(a, s);
+  switch (head_dim) {
+    case 16: return launch<32, 16>(a, s);
+    case 32: return launch<32, 32>(a, s);
+    case 64: return launch<64, 64>(a, s);
+    default: return launch<128, 128>(a, s);
+  }
 }

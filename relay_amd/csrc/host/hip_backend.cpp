@@ -104,7 +104,7 @@ class HipBackend final : public Backend {
     layout_ = {c_.layers, c_.kv_heads, c_.head_dim, block_size, num_blocks};
     if (kv_block_bytes() % 16 != 0) throw std::invalid_argument("a KV block must be a multiple of 16 bytes");
     const int D = c_.head_dim;
-    fast_attention_ = !opt_.reference_attention && (D == 64 || D == 128);
+    fast_attention_ = !opt_.reference_attention && (D == 16 || D == 32 || D == 64 || D == 128);
     if (!fast_attention_ && D > 256) throw std::invalid_argument("head_dim above 256 is not supported");
 
     load_weights(src);

@@ -60,7 +60,7 @@ def check_close(g, o, tol=2e-3):
     assert err <= tol * np.abs(o).max() + 1e-5, f"max abs err {err}, scale {np.abs(o).max()}"
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
 @pytest.mark.parametrize("heads,kv_heads", [(8, 8), (9, 3), (32, 4), (32, 8), (16, 1), (40, 2)])
 def test_matches_oracle_heads(torch_mod, dev, D, heads, kv_heads):
     case = PagedCase([1, 37, 512, 513, 1500], 1, heads, kv_heads, D, 16, seed=heads + D)
@@ -75,7 +75,8 @@ def test_context_lengths(torch_mod, dev, ctx):
     check_close(g, oracle_out(case))
 
 
-@pytest.mark.parametrize("D,slice_keys", [(64, 128), (64, 384), (64, 512), (64, 1024), (64, 2048), (64, 4096),
+@pytest.mark.parametrize("D,slice_keys", [(16, 128), (16, 1024), (32, 128), (32, 384), (32, 2048),
+                                          (64, 128), (64, 384), (64, 512), (64, 1024), (64, 2048), (64, 4096),
                                           (128, 64), (128, 192), (128, 512), (128, 1024), (128, 4096)])
 def test_slice_sizes(torch_mod, dev, D, slice_keys):
     """Every split of the context (1 to 66 slices; 4 or 8 waves) gives the same attention."""
@@ -84,9 +85,10 @@ def test_slice_sizes(torch_mod, dev, D, slice_keys):
     check_close(g, oracle_out(case))
 
 
+@pytest.mark.parametrize("D", [16, 64])
 @pytest.mark.parametrize("bs", [1, 2, 4, 8, 16, 32, 64, 12])
-def test_block_sizes(torch_mod, dev, bs):
-    case = PagedCase([5, 300, 1030], 1, 8, 2, 64, bs, seed=bs)
+def test_block_sizes(torch_mod, dev, bs, D):
+    case = PagedCase([5, 300, 1030], 1, 8, 2, D, bs, seed=bs)
     g, _ = run_decode(torch_mod, dev, case)
     check_close(g, oracle_out(case))
 

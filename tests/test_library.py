@@ -137,18 +137,20 @@ def test_prefill_plan_rejects_small_capacity():
 
 def test_work_planners_follow_their_rules():
     """The host-side planners (no device needed): rh_decode_slice_keys cuts contexts into
-    whole chunks, one slice for a handful of short contexts, at least two otherwise, never
-    below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles;
+    whole chunks, 4-chunk slices for few groups at head size 64, one slice for a handful of
+    short contexts, at least two otherwise, never below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles;
     rh_gemv_int8_row_stride pads rows that are a multiple of 2 KB."""
     L = _lib.lib()
-    for D in (64, 128):
+    for D in (16, 32, 64, 128):
         chunk = L.rh_decode_chunk_keys(D)
-        assert chunk == (64 if D == 64 else 32)
+        assert chunk == {16: 128, 32: 128, 64: 64, 128: 32}[D]
         for n, kvh, g, ctx in [(32, 4, 8, 2048), (48, 8, 4, 8192), (1, 3, 3, 640), (1, 8, 4, 65536), (200, 8, 4, 100)]:
             sk = L.rh_decode_slice_keys(n, kvh, g, D, ctx)
             assert sk > 0 and sk % chunk == 0
             groups = n * kvh * ((g + 15) // 16)
-            if groups <= 16 and ctx <= 16 * chunk:
+            if D == 64 and groups * ((ctx + 4 * chunk - 1) // (4 * chunk)) <= 256:
+                assert sk == 4 * chunk  # few groups: latency-bound, one chunk per wave of 4
+            elif groups <= 16 and ctx <= 16 * chunk:
                 assert sk >= ctx  # one slice
             else:
                 assert sk >= 8 * chunk and (ctx + sk - 1) // sk >= min(2, (ctx + 8 * chunk - 1) // (8 * chunk))

@@ -71,7 +71,7 @@ def check_close(g, o, tol=2e-3):
     assert err <= tol * np.abs(o).max() + 1e-5, f"max abs err {err}, scale {np.abs(o).max()}"
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (9, 3), (32, 4), (16, 2)])
 def test_matches_oracle(torch_mod, dev, D, heads, kv_heads):
     # whole prompts, a chunk at an offset, a 2-token chunk, tiles crossing 128-row bounds
@@ -132,5 +132,5 @@ def test_reference_kernel_matches_oracle(torch_mod, dev, D):
 def test_rejects_unsupported_head_dim(torch_mod, dev):
     from relay_amd import _lib
 
-    rc = _lib.lib().rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 4, 32, 16, 0.1, None, 64, None)
+    rc = _lib.lib().rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 4, 48, 16, 0.1, None, 64, None)
     assert rc != 0 and "head_dim" in _lib.last_error()

@@ -22,10 +22,12 @@ COMBOS = [(8, 8), (9, 3), (32, 4), (32, 8), (16, 1), (40, 2), (64, 4), (12, 4), 
 def test_random_decode(torch_mod, dev, seed):
     rng = np.random.default_rng(1000 + seed)
     h, kv = COMBOS[rng.integers(len(COMBOS))]
-    D = int(rng.choice([64, 128]))
+    D = int(rng.choice([16, 32, 64, 128]))
     bs = int(rng.choice([1, 2, 4, 8, 12, 16, 32, 64]))
     ctxs = [int(c) for c in rng.integers(1, 3000, size=int(rng.integers(1, 24)))]
-    chunk = 64 if D == 64 else 32
+    from relay_amd import _lib
+
+    chunk = _lib.lib().rh_decode_chunk_keys(D)
     sk = None if seed % 2 else chunk * int(rng.integers(1, 40))
     print(f"random decode {seed}: heads {h}/{kv} D {D} bs {bs} slice {sk} contexts {ctxs}", flush=True)
     case = PagedCase(ctxs, 1, h, kv, D, bs, seed=seed)
@@ -37,7 +39,7 @@ def test_random_decode(torch_mod, dev, seed):
 def test_random_prefill(torch_mod, dev, seed):
     rng = np.random.default_rng(2000 + seed)
     h, kv = COMBOS[rng.integers(len(COMBOS))]
-    D = int(rng.choice([64, 128]))
+    D = int(rng.choice([16, 32, 64, 128]))
     bs = int(rng.choice([1, 4, 12, 16, 32]))
     ctxs = [int(c) for c in rng.integers(2, 700, size=int(rng.integers(1, 4)))]
     new = [int(rng.integers(1, c + 1)) for c in ctxs]
