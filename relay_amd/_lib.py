@@ -141,7 +141,7 @@ def prefill_work(chunks, heads: int):
     import numpy as np
 
     cols = [np.ascontiguousarray([c[i] for c in chunks], dtype=np.int32) for i in range(4)]
-    cap = len(chunks) + sum(c[1] for c in chunks) // 128 + 1
+    cap = len(chunks) + sum(c[1] for c in chunks) // lib().rh_prefill_tile_rows() + 1
     work = np.zeros((cap, 8), dtype=np.int32)
     n = lib().rh_prefill_plan(*[c.ctypes.data for c in cols], len(chunks), heads, work.ctypes.data, cap)
     check(n if n < 0 else 0, "rh_prefill_plan")

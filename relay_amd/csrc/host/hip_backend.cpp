@@ -461,7 +461,7 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
   if (T > max_tokens_) throw std::invalid_argument("batch has more tokens than max_batch_tokens");
   // Prefill work records (heaviest first).
   const int n_chunks = static_cast<int>(pf_t0.size());
-  std::vector<int> work(8 * static_cast<std::size_t>(n_chunks + T / 128 + 1));
+  std::vector<int> work(8 * static_cast<std::size_t>(n_chunks + T / rh_prefill_tile_rows() + 1));
   const int n_work = n_chunks ? rh_prefill_plan(pf_t0.data(), pf_rows.data(), pf_pos0.data(), pf_toff.data(), n_chunks,
                                                 c_.heads, work.data(), static_cast<int>(work.size() / 8))
                               : 0;
