@@ -185,7 +185,7 @@ def _translate(msg: str) -> Exception:
     if "update_weight: int8" in msg:
         return RuntimeError(msg)
     if any(s in msg for s in ("block table too short", "max_context", "max_batch_tokens", "block id", "update_weight",
-                              "wrong size", "no backend", "logits buffer")):
+                              "wrong size", "no backend", "logits buffer", "cannot want logits")):
         return ValueError(msg)
     return _lib.RelayHipError(msg)
 

@@ -443,7 +443,12 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
       pos.push_back(ch.start_pos + i);
       seq.push_back(s);
     }
-    if (!batch.all_logits && ch.want_logits && n > 0) rows.push_back(t0 + n - 1);
+    // An empty chunk has no last row to take logits from; relay's backends would read the
+    // row before it (cuda_backend.cu:523, cpu_backend.cpp:205-206: row -1 for a leading
+    // one), so it is rejected instead of answered with an unrelated row.
+    if (!batch.all_logits && ch.want_logits && n == 0)
+      throw std::invalid_argument("a chunk with no tokens cannot want logits");
+    if (!batch.all_logits && ch.want_logits) rows.push_back(t0 + n - 1);
     // Routing: one token -> decode; more -> prefill.
     if (n == 1) {
       // (token row, context length, block-table offset): the decode kernel's descriptor

@@ -191,6 +191,12 @@ def test_errors_follow_relay_conventions(dev):
     with pytest.raises(ValueError):  # longer than max_context
         be.forward(ForwardBatch([SeqChunk([1], 100, list(range(7)), True)]))
     assert be.forward(ForwardBatch([])).shape[0] == 0
+    with pytest.raises(ValueError):  # an empty chunk that wants logits (relay's backends read another row)
+        be.forward(ForwardBatch([SeqChunk([3, 4], 0, [0], True), SeqChunk([], 0, [1], True)]))
+    # an empty chunk that wants none is skipped: same logits as without it
+    a = be.forward(ForwardBatch([SeqChunk([3, 4], 0, [0], True)]))
+    b = be.forward(ForwardBatch([SeqChunk([3, 4], 0, [0], True), SeqChunk([], 0, [1], False)]))
+    assert a.shape == b.shape and np.array_equal(a, b)
 
 
 def test_library_gemm_choices_agree(dev, monkeypatch):
