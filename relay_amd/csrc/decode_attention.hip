@@ -380,11 +380,35 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     } else {
-      for (int p = 0; p < nparts; ++p) M = fmaxf(M, coherent_load(&a.part_ml[(base + p) * 2]));
-      for (int p = 0; p < nparts; ++p) {
-        const float f = fast_exp2(coherent_load(&a.part_ml[(base + p) * 2]) - M);
-        L += f * coherent_load(&a.part_ml[(base + p) * 2 + 1]);
-        O += f * coherent_load(&a.part_o[(base + p) * DR + d]);
+      // The same arithmetic in the same order, with the loads of kMergeBatch slices issued
+      // together in each round.
+      for (int p0 = 0; p0 < nparts; p0 += kMergeBatch) {
+        float mv[kMergeBatch];
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q)
+          if (p0 + q < nparts) mv[q] = coherent_load(&a.part_ml[(base + p0 + q) * 2]);
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q)
+          if (p0 + q < nparts) M = fmaxf(M, mv[q]);
+      }
+      for (int p0 = 0; p0 < nparts; p0 += kMergeBatch) {
+        float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          if (p0 + q < nparts) {
+            mv[q] = coherent_load(&a.part_ml[(base + p0 + q) * 2]);
+            lv[q] = coherent_load(&a.part_ml[(base + p0 + q) * 2 + 1]);
+            ov[q] = coherent_load(&a.part_o[(base + p0 + q) * DR + d]);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kMergeBatch; ++q) {
+          if (p0 + q < nparts) {
+            const float f = fast_exp2(mv[q] - M);
+            L += f * lv[q];
+            O += f * ov[q];
+          }
+        }
       }
     }
     a.out[static_cast<int64_t>(t) * a.out_stride + static_cast<int64_t>(h0 + hh) * DR + d] = static_cast<half_t>(O / L);
@@ -432,10 +456,15 @@ extern "C" int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head
   // than 256 groups, but never below 8 chunks (one per wave of an 8-wave workgroup).
   const long groups = static_cast<long>(n_dec) * kv_heads * ((group + 15) / 16);
   // Head size 64 with few groups: the step is latency-bound, so slices of 4 chunks (one per
-  // wave of a 4-wave workgroup) as long as that makes at most 256 workgroups. Measured:
+  // wave of a 4-wave workgroup), longer if the context needs more than kMergeBatch of them,
+  // as long as that makes at most 256 workgroups. Measured:
   // 1 x 640 keys, 9/3 heads (config 1) 10.2 -> 6.9 us; 1 x 2048, 32/4 11.7 -> 9.0 us;
   // 8 x 2048, 32/4 12.8 -> 11.1 us. (At head size 128 the same split measured slower.)
-  if (head_dim == 64 && groups * ((max_ctx + 4 * chunk - 1) / (4 * chunk)) <= 256) return 4 * chunk;
+  // At most kMergeBatch slices, so the merge takes one round of loads.
+  if (head_dim == 64) {
+    const long small = std::max(4L * chunk, static_cast<long>((max_ctx + kMergeBatch * chunk - 1) / (kMergeBatch * chunk) * chunk));
+    if (groups * ((max_ctx + small - 1) / small) <= 256) return static_cast<int>(small);
+  }
   // A handful of short contexts: one slice (no merge); the launch is latency-bound anyway.
   if (groups <= 16 && max_ctx <= 16 * chunk) return (max_ctx + chunk - 1) / chunk * chunk;
   const long parts = std::max(2L, 256 / groups);

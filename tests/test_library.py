@@ -148,8 +148,9 @@ def test_work_planners_follow_their_rules():
             sk = L.rh_decode_slice_keys(n, kvh, g, D, ctx)
             assert sk > 0 and sk % chunk == 0
             groups = n * kvh * ((g + 15) // 16)
-            if D == 64 and groups * ((ctx + 4 * chunk - 1) // (4 * chunk)) <= 256:
-                assert sk == 4 * chunk  # few groups: latency-bound, one chunk per wave of 4
+            small = max(4 * chunk, -(-ctx // (8 * chunk)) * chunk)
+            if D == 64 and groups * -(-ctx // small) <= 256:
+                assert sk == small and -(-ctx // sk) <= 8  # few groups: short slices, one merge round
             elif groups <= 16 and ctx <= 16 * chunk:
                 assert sk >= ctx  # one slice
             else:
