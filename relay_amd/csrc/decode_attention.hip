@@ -299,11 +299,14 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
 
   // Merge the waves' partials in LDS (the V staging area, now free).
   __syncthreads();
-  float* so = reinterpret_cast<float*>(&s_v[0][0]);  // [wave][head][D]
+  // [wave][head][D], head hh's row rotated by 4 * hh floats: the 16 heads of one write
+  // instruction would otherwise all hit the same LDS banks (a 16-way conflict that
+  // serialised this store for ~1.7 us per workgroup).
+  float* so = reinterpret_cast<float*>(&s_v[0][0]);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) so[(w * 16 + c) * D + 16 * dt + 4 * g + r] = o[dt][r];
+    for (int r = 0; r < 4; ++r) so[(w * 16 + c) * D + ((16 * dt + 4 * g + 4 * c) & (D - 1)) + r] = o[dt][r];
   if (g == 0) {
     s_m[w][c] = m_run;
     s_l[w][c] = l_tot;
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2
       if (mw != -INFINITY) {
         const float f = fast_exp2(mw - M);
         L += f * s_l[ww][hh];
-        O += f * so[(ww * 16 + hh) * D + d];
+        O += f * so[(ww * 16 + hh) * D + ((d + 4 * hh) & (D - 1))];
       }
     }
     if (single) {
