@@ -93,8 +93,10 @@ struct Stage {
 // SCALAR: block_size is a power of two >= 16 (table entries are wave-uniform per tile).
 // D is the compute width, DR the head size of the cache rows, q and out: equal, except head
 // size 16, which runs at width 32 with dims 16..31 of K, V and q taken as zero.
+// Occupancy: up to D = 64 the kernel fits 128 VGPRs, so a CU holds two 8-wave workgroups
+// (4 waves per SIMD); at D = 128 it needs more and holds one.
 template <int D, int DR, int WAVES, bool SCALAR>
-__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_decode_kernel(
+__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 4 : 2, D <= 64 ? 4 : 2))) void paged_decode_kernel(
     const DecodeArgs a) {
   constexpr int SK = stage_keys<D>();
   constexpr int STEPS = SK / kStepKeys;
@@ -519,10 +521,11 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
   a.out_stride = out_row_stride;
   const int grid = (a.groups_total + 7) / 8 * 8 * max_parts;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // 8 waves when every wave gets at least two stages of a slice, else 4 (measured at
-  // config 2: 512-key slices on 8 waves run their 512 workgroups in two rounds, 24.2 us,
-  // against 18.8 us on 4 waves).
-  const bool eight = slice_keys / chunk >= 16;
+  // 8 waves when every wave gets at least one stage of a slice (D <= 64, two workgroups per
+  // CU) or two (D = 128, one per CU), else 4. Measured at config 2: 512-key slices 18.6 ->
+  // 18.3 us, 256-key slices 23.4 -> 19.6 us against 4 waves; at D = 128, 8 waves with one
+  // stage each run their workgroups in two rounds.
+  const bool eight = slice_keys / chunk >= (head_dim <= 64 ? 8 : 16);
   switch (head_dim) {
     case 16: return launch_waves<32, 16>(a, grid, eight, s);
     case 32: return launch_waves<32, 32>(a, grid, eight, s);
