@@ -64,10 +64,24 @@ __global__ void f32_to_f16_vec_kernel(const float4* in, half8* out, size_t n8) {
   }
 }
 
-__global__ void embed_kernel(const int* tokens, const half_t* table, int H, float* x) {
-  const int t = blockIdx.x;
-  const half_t* row = table + static_cast<int64_t>(tokens[t]) * H;
-  for (int i = threadIdx.x; i < H; i += blockDim.x) x[static_cast<int64_t>(t) * H + i] = static_cast<float>(row[i]);
+// x[t][c] = fp32(table[tokens[t]][c]) over the flat index of x, VEC consecutive elements per
+// thread and step (8 -- one 16-byte load, two 16-byte stores -- when H % 8 == 0, else 1).
+template <int VEC>
+__global__ void embed_kernel(const int* tokens, const half_t* table, int H, int64_t n_vec, float* x) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_vec; i += stride) {
+    const int64_t e = i * VEC;
+    const int t = static_cast<int>(e / H), col = static_cast<int>(e - static_cast<int64_t>(t) * H);
+    const half_t* src = table + static_cast<int64_t>(tokens[t]) * H + col;
+    if (VEC == 8) {
+      const half8 h = load_half8(src);
+      float4* dst = reinterpret_cast<float4*>(x + e);
+      dst[0] = float4{static_cast<float>(h[0]), static_cast<float>(h[1]), static_cast<float>(h[2]), static_cast<float>(h[3])};
+      dst[1] = float4{static_cast<float>(h[4]), static_cast<float>(h[5]), static_cast<float>(h[6]), static_cast<float>(h[7])};
+    } else {
+      x[e] = static_cast<float>(*src);
+    }
+  }
 }
 
 // Sum of squares in double, as the fp32 CPU backend does (cpu_backend.cpp:47-52).
@@ -193,18 +207,21 @@ __global__ void silu_mul_vec_kernel(const float* gu, int I, half_t* act) {
   *reinterpret_cast<half8*>(act + static_cast<int64_t>(t) * I + i) = r;
 }
 
-__global__ void kv_gather_kernel(const uint4v* k, const uint4v* v, const int* blocks, int n, int64_t vecs, uint4v* out) {
-  const int i = blockIdx.x, which = blockIdx.y;
-  const uint4v* src = (which ? v : k) + static_cast<int64_t>(blocks[i]) * vecs;
-  uint4v* dst = out + (static_cast<int64_t>(which) * n + i) * vecs;
-  for (int64_t e = threadIdx.x; e < vecs; e += kThreads) dst[e] = src[e];
-}
-
-__global__ void kv_scatter_kernel(uint4v* k, uint4v* v, const int* blocks, int n, int64_t vecs, const uint4v* in) {
-  const int i = blockIdx.x, which = blockIdx.y;
-  uint4v* dst = (which ? v : k) + static_cast<int64_t>(blocks[i]) * vecs;
-  const uint4v* src = in + (static_cast<int64_t>(which) * n + i) * vecs;
-  for (int64_t e = threadIdx.x; e < vecs; e += kThreads) dst[e] = src[e];
+// The K and V runs of n cache blocks against a packed buffer [K of blocks[0..n)][V of
+// blocks[0..n)] (relay's transfer format): one grid-stride loop over the buffer's 16-byte
+// vectors, so consecutive threads touch consecutive bytes of the buffer whatever the block
+// size. TO_BUF: pools -> buffer (gather), else buffer -> pools (scatter).
+template <bool TO_BUF>
+__global__ void kv_pack_kernel(uint4v* k, uint4v* v, const int* blocks, int n, int64_t vecs, uint4v* buf) {
+  const int64_t total = 2 * static_cast<int64_t>(n) * vecs;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t piece = e / vecs;
+    const bool is_v = piece >= n;
+    uint4v* pool = (is_v ? v : k) + static_cast<int64_t>(blocks[is_v ? piece - n : piece]) * vecs + (e - piece * vecs);
+    if (TO_BUF) buf[e] = *pool;
+    else *pool = buf[e];
+  }
 }
 
 // One wave per row: scale = max|w| / 127 (1 for a zero row), q = rint(w / scale).
@@ -360,8 +377,15 @@ int rh_f32_to_f16(const float* in, void* out, size_t n, void* stream) {
 int rh_embed(const int* tokens, int T, const void* table, int H, float* x, void* stream) {
   if (T == 0) return 0;
   RH_REQUIRE(T > 0 && H > 0, "embed: bad shape");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), tokens,
-                                   static_cast<const half_t*>(table), H, x));
+  const int64_t n = static_cast<int64_t>(T) * H;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (H % 8 == 0 && reinterpret_cast<uintptr_t>(table) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(embed_kernel<8>, dim3(grid_for(n / 8)), dim3(kThreads), 0, s, tokens,
+                                     static_cast<const half_t*>(table), H, n / 8, x));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(embed_kernel<1>, dim3(grid_for(n)), dim3(kThreads), 0, s, tokens,
+                                     static_cast<const half_t*>(table), H, n, x));
+  }
   return 0;
 }
 
@@ -423,9 +447,11 @@ int rh_kv_gather(const void* kpool, const void* vpool, const int* blocks, int n,
                  void* stream) {
   if (n == 0) return 0;
   RH_REQUIRE(n > 0 && block_bytes % 16 == 0, "kv_gather: block bytes must be a multiple of 16");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_gather_kernel, dim3(n, 2), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                                   static_cast<const uint4v*>(kpool), static_cast<const uint4v*>(vpool), blocks, n,
-                                   static_cast<int64_t>(block_bytes / 16), static_cast<uint4v*>(buf)));
+  const int64_t vecs = static_cast<int64_t>(block_bytes / 16);
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_pack_kernel<true>, dim3(grid_for(2 * n * vecs)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), static_cast<uint4v*>(const_cast<void*>(kpool)),
+                                   static_cast<uint4v*>(const_cast<void*>(vpool)), blocks, n, vecs,
+                                   static_cast<uint4v*>(buf)));
   return 0;
 }
 
@@ -433,9 +459,11 @@ int rh_kv_scatter(void* kpool, void* vpool, const int* blocks, int n, size_t blo
                   void* stream) {
   if (n == 0) return 0;
   RH_REQUIRE(n > 0 && block_bytes % 16 == 0, "kv_scatter: block bytes must be a multiple of 16");
-  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_scatter_kernel, dim3(n, 2), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                                   static_cast<uint4v*>(kpool), static_cast<uint4v*>(vpool), blocks, n,
-                                   static_cast<int64_t>(block_bytes / 16), static_cast<const uint4v*>(buf)));
+  const int64_t vecs = static_cast<int64_t>(block_bytes / 16);
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(kv_pack_kernel<false>, dim3(grid_for(2 * n * vecs)), dim3(kThreads), 0,
+                                   static_cast<hipStream_t>(stream), static_cast<uint4v*>(kpool),
+                                   static_cast<uint4v*>(vpool), blocks, n, vecs,
+                                   static_cast<uint4v*>(const_cast<void*>(buf))));
   return 0;
 }
 
