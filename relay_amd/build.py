@@ -74,6 +74,8 @@ def build_oracle() -> None:
     subprocess.run(["make", "-s", "-C", oracle, "-B", "all"], check=True)
     if os.path.isdir("/root/reference/engine"):
         subprocess.run(["make", "-s", "-C", oracle, "-j8", "ref"], check=True)
+        # relay's Engine driving the HIP backend (needs the kernel objects of build())
+        subprocess.run(["make", "-s", "-C", oracle, "-j8", "engine-hip"], check=True)
 
 
 if __name__ == "__main__":
