@@ -460,15 +460,16 @@ extern "C" int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head
   // context (enough workgroups to spread over the 256 CUs), more while there are fewer
   // than 256 groups, but never below 8 chunks (one per wave of an 8-wave workgroup).
   const long groups = static_cast<long>(n_dec) * kv_heads * ((group + 15) / 16);
-  // Head size 64 with few groups: the step is latency-bound, so slices of 4 chunks (one per
-  // wave of a 4-wave workgroup), longer if the context needs more than kMergeBatch of them,
-  // as long as that makes at most 256 workgroups. Measured:
-  // 1 x 640 keys, 9/3 heads (config 1) 10.2 -> 6.9 us; 1 x 2048, 32/4 11.7 -> 9.0 us;
-  // 8 x 2048, 32/4 12.8 -> 11.1 us. (At head size 128 the same split measured slower.)
-  // At most kMergeBatch slices, so the merge takes one round of loads.
-  if (head_dim == 64) {
-    const long small = std::max(4L * chunk, static_cast<long>((max_ctx + kMergeBatch * chunk - 1) / (kMergeBatch * chunk) * chunk));
-    if (groups * ((max_ctx + small - 1) / small) <= 256) return static_cast<int>(small);
+  // Head size 64 or 128 with few groups: the step is latency-bound, so kMergeBatch slices
+  // per context (the merge then takes one round of loads), of 2 to 8 chunks, as long as that
+  // makes at most 256 workgroups (longer contexts take the rule below: enough workgroups
+  // to stream from HBM); the launcher gives them 8 waves from 4 chunks on.
+  // Measured (us, against the earlier 4-chunk minimum on 4 waves): 1 x 640 keys, 9/3 heads
+  // (config 1) 6.87 -> 6.16; 1 x 2048, 32/4 8.57 -> 8.12; 8 x 2048, 32/4 10.78 -> 10.19;
+  // 1 x 2048, 32/8, D128 11.65 -> 10.41.
+  if (head_dim == 64 || head_dim == 128) {
+    const long small = std::max(2L * chunk, static_cast<long>((max_ctx + kMergeBatch * chunk - 1) / (kMergeBatch * chunk) * chunk));
+    if (small <= 8L * chunk && groups * ((max_ctx + small - 1) / small) <= 256) return static_cast<int>(small);
   }
   // A handful of short contexts: one slice (no merge); the launch is latency-bound anyway.
   if (groups <= 16 && max_ctx <= 16 * chunk) return (max_ctx + chunk - 1) / chunk * chunk;
@@ -525,7 +526,11 @@ extern "C" int rh_paged_decode_attention(const void* q, int64_t q_row_stride, co
   // CU) or two (D = 128, one per CU), else 4. Measured at config 2: 512-key slices 18.6 ->
   // 18.3 us, 256-key slices 23.4 -> 19.6 us against 4 waves; at D = 128, 8 waves with one
   // stage each run their workgroups in two rounds.
-  const bool eight = slice_keys / chunk >= (head_dim <= 64 ? 8 : 16);
+  // A grid of at most 256 workgroups (one round on the CUs: a latency-bound launch) takes 8
+  // waves from 4 stages per slice on (1 x 2048 keys: 8.57 -> 8.12 us at D64, 11.65 -> 10.41
+  // at D128; slices of 2 stages stay on 4 waves: 6.16 against 6.32 us at 1 x 640).
+  const int stages = slice_keys / chunk;
+  const bool eight = stages >= (head_dim <= 64 ? 8 : 16) || (stages >= 4 && grid <= 256);
   switch (head_dim) {
     case 16: return launch_waves<32, 16>(a, grid, eight, s);
     case 32: return launch_waves<32, 32>(a, grid, eight, s);

@@ -137,7 +137,8 @@ def test_prefill_plan_rejects_small_capacity():
 
 def test_work_planners_follow_their_rules():
     """The host-side planners (no device needed): rh_decode_slice_keys cuts contexts into
-    whole chunks, 4-chunk slices for few groups at head size 64, one slice for a handful of
+    whole chunks, kMergeBatch (8) slices of 2 to 8 chunks for few groups at head sizes 64 and
+    128, one slice for a handful of
     short contexts, at least two otherwise, never below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles;
     rh_gemv_int8_row_stride pads rows that are a multiple of 2 KB."""
     L = _lib.lib()
@@ -148,14 +149,16 @@ def test_work_planners_follow_their_rules():
             sk = L.rh_decode_slice_keys(n, kvh, g, D, ctx)
             assert sk > 0 and sk % chunk == 0
             groups = n * kvh * ((g + 15) // 16)
-            small = max(4 * chunk, -(-ctx // (8 * chunk)) * chunk)
-            if D == 64 and groups * -(-ctx // small) <= 256:
+            small = max(2 * chunk, -(-ctx // (8 * chunk)) * chunk)
+            if D in (64, 128) and small <= 8 * chunk and groups * -(-ctx // small) <= 256:
                 assert sk == small and -(-ctx // sk) <= 8  # few groups: short slices, one merge round
             elif groups <= 16 and ctx <= 16 * chunk:
                 assert sk >= ctx  # one slice
             else:
                 assert sk >= 8 * chunk and (ctx + sk - 1) // sk >= min(2, (ctx + 8 * chunk - 1) // (8 * chunk))
     assert L.rh_decode_slice_keys(32, 4, 8, 64, 2048) == 1024  # config 2: two slices of 1024 keys
+    assert L.rh_decode_slice_keys(1, 3, 3, 64, 640) == 128  # config 1: five slices of 2 chunks
+    assert L.rh_decode_slice_keys(1, 8, 4, 128, 2048) == 256  # 8 slices of 8 chunks at D128
     assert L.rh_decode_chunk_keys(96) == -1
     assert [L.rh_gemv_f16_split_plan(T, K, N) for T, K, N in
             [(32, 5632, 2048), (1, 5632, 2048), (32, 2048, 2048), (32, 4096, 4096), (8, 14336, 4096), (1, 4096, 1024)]] \
