@@ -202,11 +202,11 @@ def bench_gemv(torch, dev, stream, steps, warmup, Ts=(1, 4, 8)):
 
 # ---- config 3b: TinyLlama decode step --------------------------------------------------
 
-def bench_tinyllama_decode(steps, int8=False, n_seq=32, ctx=2048):
-    from relay_amd import HipBackend, HipOptions, tinyllama_1b
+def bench_tinyllama_decode(steps, int8=False, n_seq=32, ctx=2048, model="tinyllama"):
+    from relay_amd import HipBackend, HipOptions, smollm2_135m, tinyllama_1b
     from relay_amd.backend import ForwardBatch, SeqChunk
 
-    c = tinyllama_1b()
+    c = smollm2_135m() if model == "smollm2" else tinyllama_1b()
     bs = 16
     per = (ctx + 64 + bs - 1) // bs
     be = HipBackend(None, n_seq * per + 1, bs, max_batch_tokens=512, max_context=per * bs,
@@ -570,6 +570,8 @@ def main():
                     help="run only this part (for profiling) and print its numbers as one JSON line")
     ap.add_argument("--nseq", type=int, default=32, help="--leg tinyllama: decode batch")
     ap.add_argument("--ctx", type=int, default=2048, help="--leg tinyllama: context")
+    ap.add_argument("--model", choices=["tinyllama", "smollm2"], default="tinyllama",
+                    help="--leg tinyllama: the model shape (SmolLM2-135M for config 1's layers)")
     ap.add_argument("--int8", action="store_true", help="--leg tinyllama: int8 weights")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 20 times (the known-size kernel that scales the "
@@ -606,7 +608,7 @@ def main():
         elif args.leg == "config1":
             r = bench_config1()
         elif args.leg == "tinyllama":
-            r = bench_tinyllama_decode(args.steps, int8=args.int8, n_seq=args.nseq, ctx=args.ctx)
+            r = bench_tinyllama_decode(args.steps, int8=args.int8, n_seq=args.nseq, ctx=args.ctx, model=args.model)
         elif args.leg == "refpoints":
             r = bench_reference_points(max(1, min(args.steps, 10)))
         elif args.leg == "tinyllamaprefill":

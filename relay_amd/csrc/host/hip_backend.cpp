@@ -344,11 +344,11 @@ void HipBackend::load_weights(const WeightSource& src) {
 }
 
 void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta) {
-  // Decode batch sizes: the skinny MFMA product (the library GEMM spends ~8-12 us per call on
-  // small matrices). Up to 16 tokens for every matrix; at 17-32 tokens only up to N = 4096,
-  // where it is ahead (TinyLlama shapes at T = 32: qkv 2560 x 2048 8.8 vs 12.0 us, wo 8.7 vs
-  // 12.0, down 2048 x 5632 with K split in two 14.4 vs 16.2) and the library kernels win on
-  // the wider gate_up (21.6 vs 15.9 us) and lm_head.
+  // Decode batch sizes up to 16 tokens: the skinny MFMA product; above, the library's timed
+  // choice. Measured on whole decode steps (ms per step, skinny / library for every plain
+  // product): TinyLlama 1.38 / 1.42 at 8 tokens, 1.51 / 1.45 at 16, 1.88 / 1.67 at 24,
+  // 2.06 / 1.70 at 32; SmolLM2-135M 1.16 / 1.28 at 8, 1.60 / 1.70 at 16, 1.66 / 1.50 at 32;
+  // one token: config 1's step 0.85 against 1.75 ms.
   if (skinny(K, N, T)) {
     const int ks = rh_gemv_f16_split_plan(T, K, N);
     if (ks > 1) {
@@ -375,13 +375,15 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
                                 rocblas_gemm_algo_standard, 0, 0));
 }
 
-bool HipBackend::skinny(int K, int N, int T) {
-  return K % 16 == 0 && (T <= 16 || (T <= rh_gemv_f16_max_tokens() && N <= 4096));
-}
+bool HipBackend::skinny(int K, int N, int T) { return K % 16 == 0 && T <= 16; }
 
 bool HipBackend::fused(const DeviceMatrix& W, int T) const {
-  // Normalisation / activation folded into the skinny fp16 product (same T range as gemm_f16's).
-  return !W.i8.p && T <= 16 && W.K % 16 == 0 && rh_gemv_f16_fused_fits(T, W.K);
+  // Normalisation / activation folded into the skinny fp16 product, up to 16 tokens, when its
+  // 16-row tiles fit one round of workgroups on the CUs: every workgroup repeats the
+  // prologue, so on wider matrices the repeats cost more than the launch they save (TinyLlama
+  // gate_up, 704 tiles, at T = 8: 27.7 us fused against 3.7 + 13.8 us for RMSNorm and the
+  // library product).
+  return !W.i8.p && T <= 16 && W.K % 16 == 0 && (W.N + 15) / 16 <= 256 && rh_gemv_f16_fused_fits(T, W.K);
 }
 
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
@@ -533,7 +535,10 @@ std::vector<float> HipBackend::forward(const ForwardBatch& batch, LayerObserver*
       RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
                                        d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
                                        layout_.block_size, stream_));
-    } else if (!L.wqkv.i8.p && D % 16 == 0 && skinny(H, QKV, T) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
+    } else if (!L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 &&
+               (T <= 16 || (T <= rh_gemv_f16_max_tokens() && QKV <= 4096)) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
+      // (17-32 tokens: TinyLlama's 2560-row qkv 11.1 us here against 9.5 + 3.0 us for the
+      // library product and a separate qkv_post.)
       // The projection and qkv_post in one launch (the RMSNorm cannot be folded in here).
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_f16_qkv(L.wqkv.f16.p, H, xn_.p, qkv_.p, T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab,
