@@ -67,18 +67,24 @@ template <int WAVES, int NB, int RT, bool F16_SCALE>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                   const void* __restrict__ scale,
                                                                   const half_t* __restrict__ x, float* y, int T,
-                                                                  int K, int N, float beta) {
-  constexpr int U = NB == 1 ? kUnroll : (NB == 2 ? 2 : 1);
+                                                                  int K, int N, float beta, int rows_per) {
+  constexpr int U = NB == 1 ? (RT <= 2 ? kUnroll : 2) : (NB == 2 ? 2 : 1);
   __shared__ float red[WAVES][RT][NB][kWave * 4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * RT;
+  // Rows [n0, nl) of W: rows_per <= 16 RT rows per workgroup (the last tile may be partly
+  // empty: its rows load nothing and store nothing).
+  const int n0 = blockIdx.x * rows_per, nl = min(N, n0 + rows_per);
   const int nchunks = (K + kChunk - 1) / kChunk;
   const int per = (nchunks + WAVES - 1) / WAVES;
   const int cb = w * per, ce = min(nchunks, cb + per);
   const int8_t* wrow[RT];
+  bool rv[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) wrow[rt] = w8 + static_cast<int64_t>(min(n0 + 16 * rt + c, N - 1)) * ldw;
+  for (int rt = 0; rt < RT; ++rt) {
+    wrow[rt] = w8 + static_cast<int64_t>(min(n0 + 16 * rt + c, N - 1)) * ldw;
+    rv[rt] = n0 + 16 * rt + c < nl;
+  }
   bool tok[NB];
   const half_t* xrow[NB];
 #pragma unroll
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
       const bool live = q0 + u < ce && k < K;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
-        wv[rt][u] = live ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
+        wv[rt][u] = live && rv[rt] ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
@@ -163,7 +169,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = n0 + 16 * rt + 4 * g + r;
-        if (n >= N) continue;
+        if (n >= nl) continue;
         float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
         *dst = s[r] * sc[rt][r] + (beta != 0.0f ? beta * (kEarlyY ? yold[rt][b][r] : *dst) : 0.0f);
       }
@@ -504,16 +510,23 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 
 template <int NB, int RT, bool F16_SCALE>
 int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
-              float beta, hipStream_t s) {
-  const int tiles = (N + 16 * RT - 1) / (16 * RT);
+              float beta, hipStream_t s, int rows_per = 16 * RT) {
+  const int tiles = (N + rows_per - 1) / rows_per;
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, NB, RT, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s,
-                                     w8, ldw, scale, x, y, T, K, N, beta));
+                                     w8, ldw, scale, x, y, T, K, N, beta, rows_per));
   } else {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, NB, RT, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s,
-                                     w8, ldw, scale, x, y, T, K, N, beta));
+                                     w8, ldw, scale, x, y, T, K, N, beta, rows_per));
   }
   return 0;
+}
+
+// Rows per workgroup that split n rows evenly over whole rounds of 256 workgroups (one per
+// CU), each at most `cap` rows: ceil(n / (256 k)) for the smallest such k.
+int even_rows(int n, int cap) {
+  const int k = (n + 256 * cap - 1) / (256 * cap);
+  return (n + 256 * k - 1) / (256 * k);
 }
 
 template <bool F16_SCALE>
@@ -525,6 +538,27 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
   // N = 14336, 17.1 -> 16.5 us (T = 4), 19.6 -> 17.8 (8), 26.0 -> 20.9 (16), while at T <= 2
   // or on N <= 4096 it is level or slower.
   const bool tall = (N + 31) / 32 >= 192;
+  // More row tiles than CUs: rows are split evenly over whole rounds of 256 workgroups
+  // (14336 rows in 896 tiles left half the CUs one tile more than the others: 15.0 us at
+  // T = 1, 12288 rows in 768 tiles took 11.6). Measured on 4096-column matrices (us):
+  // T = 1: 14-row workgroups at N = 14336 15.0 -> 14.4, 12-row at N = 6144 9.1 -> 8.6;
+  // T = 4-8: the two-tile workgroups, N = 14336 16.6 -> 15.5 (T = 4), 17.9 -> 17.0 (8), N =
+  // 6144 10.1 -> 8.8 (4); T = 9-16: up to four tiles in 8-row steps (one round), N = 12288
+  // 18.8 -> 15.1, 14336 21.0 -> 18.3, 28672 32.1 -> 28.0 at T = 16.
+  if (T <= 16 && (N + 15) / 16 > 256) {
+    if (T >= 9) {
+      const int units = (N + 7) / 8, m = (units + 2047) / 2048;  // rounds of 256: <= 64 rows each
+      const int rows_per = 8 * ((units + 256 * m - 1) / (256 * m));
+      switch ((rows_per + 15) / 16) {
+        case 1: return launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, rows_per);
+        case 2: return launch_nb<1, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, rows_per);
+        case 3: return launch_nb<1, 3, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, rows_per);
+        default: return launch_nb<1, 4, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, rows_per);
+      }
+    }
+    if (T >= 4 && tall) return launch_nb<1, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, even_rows(N, 32));
+    return launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s, even_rows(N, 16));
+  }
   if (T <= 16) return tall && T >= 4 ? launch_nb<1, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)
                                      : launch_nb<1, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
   if (T <= 32) return tall ? launch_nb<2, 2, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s)

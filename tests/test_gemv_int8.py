@@ -64,6 +64,21 @@ def test_matches_oracle(torch_mod, dev, T, N, K):
     assert (np.abs(y - exact) <= bound(w8, s, x)).all()
 
 
+@pytest.mark.parametrize("T", [1, 3, 4, 8, 9, 16])
+@pytest.mark.parametrize("N", [4104, 4352, 11264, 14336, 28680, 57352])
+def test_rows_split_evenly_over_the_cus(torch_mod, dev, T, N):
+    """More row tiles than CUs: each workgroup takes an even share of rows (14, 24, 56 ...),
+    so the last 16-row tile of a workgroup may be partly empty; every row must be computed
+    once (y starts as NaN) and no row of a neighbour written."""
+    K = 256
+    w8, scale, x = make(N, K, T, seed=N + T)
+    y0 = np.full((T, N), 0.5, np.float32)
+    y = run(torch_mod, dev, w8, scale, x, beta=1.0, y0=y0)
+    exact = O.gemv_int8(w8, scale, x, beta=1.0, y0=y0)
+    assert np.isfinite(y).all()
+    assert (np.abs(y - exact) <= bound(w8, scale, x) + 2 * EPS32 * np.abs(exact)).all()
+
+
 def test_beta_accumulates(torch_mod, dev):
     w8, s, x = make(300, 512, 5, seed=1)
     y0 = np.random.default_rng(2).standard_normal((5, 300)).astype(np.float32)
