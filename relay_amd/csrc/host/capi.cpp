@@ -22,6 +22,7 @@ namespace hip_detail {
 Backend* new_backend(const ModelConfig& c, const rh_host_weights* hw, bool synthetic, std::uint64_t seed, float std,
                      int num_blocks, int block_size, int device, int max_tokens, int max_context, HipOptions o);
 double last_forward_ms(const Backend* b);
+int forward_into(Backend* b, const ForwardBatch& batch, float* dst, std::size_t cap);
 void fill_kv_random(Backend* b, std::uint64_t seed, float std);
 }  // namespace hip_detail
 }  // namespace relay
@@ -154,10 +155,9 @@ int relay_hip_backend_forward(relay_hip_backend* b, int n_seqs, const int* n_tok
       tp += n_tokens[s];
       bp += table_len[s];
     }
-    std::vector<float> lg = b->be->forward(batch);
-    if (lg.size() > logits_cap) throw std::invalid_argument("logits buffer too small");
-    if (!lg.empty()) std::memcpy(logits, lg.data(), lg.size() * 4);
-    rows = static_cast<int>(lg.size() / b->be->config().vocab);
+    // Straight into the caller's buffer (relay's forward() returns a vector, which would be
+    // one more copy of every logits row).
+    rows = relay::hip_detail::forward_into(b->be, batch, logits, logits_cap);
   });
   return rc ? -1 : rows;
 }
