@@ -158,6 +158,26 @@ int64_t rh_gemv_int8_row_stride(int K);
 /* Largest T rh_gemv_int8 takes. */
 int rh_gemv_int8_max_tokens(void);
 
+/* rh_gemv_int8 with the producer of x or qkv_post folded in, for 1 <= T <= 16 (no
+ * counterpart in relay, where rms_norm_kernel, silu_mul_kernel and qkv_post run as their own
+ * launches around the GEMV, cuda_backend.cu:575-591): the int8 counterparts of
+ * rh_gemv_f16_rmsnorm, rh_gemv_f16_silu, rh_gemv_f16_qkv and rh_gemv_f16_rmsnorm_qkv, with
+ * their operands and limits (rh_gemv_f16_fused_fits(T, K) for the fused producers) and
+ * rh_gemv_int8's weights and scales. Each gives the bits of the launches it replaces. */
+int rh_gemv_int8_rmsnorm(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
+                         const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream);
+int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* gu, float* y,
+                      int T, int K, int N, float beta, void* stream);
+int rh_gemv_int8_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x, float* qkv,
+                     int T, int K, const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                     const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
+                     int kv_heads, int head_dim, int block_size, void* stream);
+int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
+                             const float* norm_w, float eps, float* qkv, int T, int K, const float* bias,
+                             const float* inv_freq, const int* pos, const int* seq, const int* table_off,
+                             const int* tables, void* kpool, void* vpool, void* q_out, int heads, int kv_heads,
+                             int head_dim, int block_size, void* stream);
+
 /* y[t, n] = sum_k W16[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for 1 <= T <= 32:
  * the dense projection at decode batch sizes. W16 fp16 [N, K] rows ldw elements apart
  * (ldw >= K, a multiple of 8); x fp16 [T, K]; y fp32 [T, N]; K a multiple of 16; W16 and x

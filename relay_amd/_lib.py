@@ -58,6 +58,10 @@ SIGNATURES = {
     "rh_prefill_tile_rows": (I, []),
     "rh_reference_attention": (I, [P, I64, P, P, P, P, P, P, P, I, I, I, I, I, F, P, I64, P]),
     "rh_gemv_int8": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
+    "rh_gemv_int8_rmsnorm": (I, [P, I64, P, I, P, P, F, P, I, I, I, F, P]),
+    "rh_gemv_int8_silu": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
+    "rh_gemv_int8_qkv": (I, [P, I64, P, I, P, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_gemv_int8_rmsnorm_qkv": (I, [P, I64, P, I, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
     "rh_gemv_int8_row_stride": (I64, [I]),
     "rh_gemv_f16": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_splitk": (I, [P, I64, P, P, I, I, I, F, I, P, P, P]),

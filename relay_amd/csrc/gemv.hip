@@ -58,124 +58,6 @@ __device__ __forceinline__ half8 int8x8_to_half8(uint32_t lo, uint32_t hi) {
   return v - bias;
 }
 
-// T <= 16 * NB tokens: NB column blocks of 16 tokens share each converted A operand, and
-// RT 16-row tiles share each activation operand (a workgroup covers 16 RT rows: above 16
-// tokens every workgroup re-reads all T activation rows of K through L2, so fewer, taller
-// workgroups read less). Fewer chunks per load batch as NB grows keeps the operands in
-// registers.
-template <int WAVES, int NB, int RT, bool F16_SCALE>
-__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
-                                                                  const void* __restrict__ scale,
-                                                                  const half_t* __restrict__ x, float* y, int T,
-                                                                  int K, int N, float beta, int rows_per) {
-  constexpr int U = NB == 1 ? (RT <= 2 ? kUnroll : 2) : (NB == 2 ? 2 : 1);
-  __shared__ float red[WAVES][RT][NB][kWave * 4];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = lane & 15, g = lane >> 4;
-  // Rows [n0, nl) of W: rows_per <= 16 RT rows per workgroup (the last tile may be partly
-  // empty: its rows load nothing and store nothing).
-  const int n0 = blockIdx.x * rows_per, nl = min(N, n0 + rows_per);
-  const int nchunks = (K + kChunk - 1) / kChunk;
-  const int per = (nchunks + WAVES - 1) / WAVES;
-  const int cb = w * per, ce = min(nchunks, cb + per);
-  const int8_t* wrow[RT];
-  bool rv[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    wrow[rt] = w8 + static_cast<int64_t>(min(n0 + 16 * rt + c, N - 1)) * ldw;
-    rv[rt] = n0 + 16 * rt + c < nl;
-  }
-  bool tok[NB];
-  const half_t* xrow[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    tok[b] = 16 * b + c < T;
-    xrow[b] = x + static_cast<int64_t>(tok[b] ? 16 * b + c : 0) * K;
-  }
-  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-
-  // Wave 0 writes the results. Its row scales (and the old y for beta != 0, where the
-  // registers allow) are loaded before the weights: issued after the reduction they would
-  // queue behind the weight stream (measured 0.7-3.8 us of dependent-load tail).
-  constexpr bool kEarlyY = NB * RT <= 2;
-  float sc[RT][4], yold[RT][NB][4];
-  if (w == 0) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = min(n0 + 16 * rt + 4 * g + r, N - 1);
-        if (F16_SCALE) sc[rt][r] = static_cast<float>(static_cast<const half_t*>(scale)[n]);
-        else sc[rt][r] = static_cast<const float*>(scale)[n];
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-          yold[rt][b][r] = kEarlyY && beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + n] : 0.0f;
-      }
-  }
-
-  float4v acc[RT][NB];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[rt][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int q0 = cb; q0 < ce; q0 += U) {
-    uint4v wv[RT][U];
-    half8 xa[NB][U], xb[NB][U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (q0 + u) * kChunk + 16 * g;
-      const bool live = q0 + u < ce && k < K;
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-        wv[rt][u] = live && rv[rt] ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
-        xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const half8 a0 = int8x8_to_half8(wv[rt][u][0], wv[rt][u][1]);
-        const half8 a1 = int8x8_to_half8(wv[rt][u][2], wv[rt][u][3]);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          acc[rt][b] = mfma16x16x32(a0, xa[b][u], acc[rt][b]);
-          acc[rt][b] = mfma16x16x32(a1, xb[b][u], acc[rt][b]);
-        }
-      }
-  }
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[w][rt][b][lane * 4 + r] = acc[rt][b][r];
-  __syncthreads();
-  if (w != 0) return;
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      // Lane (c, g) sums the waves for token 16b + c, rows n0 + 16 rt + 4g + r, in a fixed order.
-      float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ww = 0; ww < WAVES; ++ww)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[r] += red[ww][rt][b][lane * 4 + r];
-      if (!tok[b]) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = n0 + 16 * rt + 4 * g + r;
-        if (n >= nl) continue;
-        float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
-        *dst = s[r] * sc[rt][r] + (beta != 0.0f ? beta * (kEarlyY ? yold[rt][b][r] : *dst) : 0.0f);
-      }
-    }
-}
-
 // What the fp16 kernel's B operands are made from:
 //   kPlain   x fp16 [T, K], loaded per lane;
 //   kRmsNorm x fp32 [T, K] (the residual stream): fp16(w[k] * (x * 1/sqrt(mean(x^2) + eps)))
@@ -267,6 +149,284 @@ __device__ __forceinline__ void rope_epilogue(const RopeArgs& ra, const float (&
   }
 }
 
+// The B operands of a fused product, computed once per workgroup into LDS (sxb rows K + 8
+// halves apart) by all WAVES waves: RMSNorm of x (kRmsNorm) or SiLU(gate) * up (kSiluMul).
+// K is a multiple of 16 and the rows 16-byte aligned, so every thread moves whole float4
+// groups, up to kStageVec of them per batch (fewer where the kernel's 128-VGPR budget of
+// 16-wave workgroups would spill) with all their loads issued together: a chain of dependent load rounds here
+// is latency the product waits for (the first version's element loops took ~10 us at
+// T = 4, K = 5632). Ends with a barrier.
+
+__device__ __forceinline__ void store_half4(half_t* dst, half_t a, half_t b, half_t c, half_t d) {
+  *reinterpret_cast<half4*>(dst) = half4{a, b, c, d};
+}
+
+template <int PRO, int WAVES, int kStageVec>
+__device__ __forceinline__ void stage_operands(const void* xin, const float* norm_w, float eps, int T, int K,
+                                               half_t* sxb, float* s_inv) {
+  constexpr int NT = WAVES * kWave;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int XR = K + 8, K4 = K / 4, n4 = T * K4;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  if (PRO == kRmsNorm) {
+    const f4* x4 = static_cast<const f4*>(xin);
+    const f4* w4 = reinterpret_cast<const f4*>(norm_w);
+    // The first batch of staged inputs is loaded with the sums' loads (one round of loads
+    // before the barrier instead of two).
+    f4 vx[kStageVec], vw[kStageVec];
+#pragma unroll
+    for (int j = 0; j < kStageVec; ++j) {
+      const int idx = threadIdx.x + j * NT;
+      if (idx < n4) {
+        vx[j] = x4[idx];
+        vw[j] = w4[idx % K4];
+      }
+    }
+    // Sum of squares of each row in double (rh_rmsnorm's arithmetic; the order of a double
+    // sum of fp32 squares does not reach the fp32 result), one wave per row.
+    for (int t = w; t < T; t += WAVES) {
+      double ss = 0;
+#pragma unroll 8
+      for (int i = lane; i < K4; i += kWave) {
+        const f4 v = x4[static_cast<int64_t>(t) * K4 + i];
+        ss += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y + static_cast<double>(v.z) * v.z +
+              static_cast<double>(v.w) * v.w;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      if (lane == 0) s_inv[t] = 1.0f / sqrtf(static_cast<float>(ss / K) + eps);
+    }
+    __syncthreads();
+    for (int b0 = 0; b0 < n4; b0 += kStageVec * NT) {
+      if (b0 > 0) {
+#pragma unroll
+        for (int j = 0; j < kStageVec; ++j) {
+          const int idx = b0 + threadIdx.x + j * NT;
+          if (idx < n4) {
+            vx[j] = x4[idx];
+            vw[j] = w4[idx % K4];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kStageVec; ++j) {
+        const int idx = b0 + threadIdx.x + j * NT;
+        if (idx < n4) {
+          const int t = idx / K4, i = 4 * (idx - t * K4);
+          const float inv = s_inv[t];
+          store_half4(sxb + t * XR + i, f16_of_product(vw[j].x, vx[j].x * inv),
+                             f16_of_product(vw[j].y, vx[j].y * inv), f16_of_product(vw[j].z, vx[j].z * inv),
+                             f16_of_product(vw[j].w, vx[j].w * inv));
+        }
+      }
+    }
+    __syncthreads();
+  } else if (PRO == kSiluMul) {
+    const f4* gu4 = static_cast<const f4*>(xin);  // [T][2 K4]: gate | up
+    for (int b0 = 0; b0 < n4; b0 += kStageVec * NT) {
+      f4 vg[kStageVec], vu[kStageVec];
+#pragma unroll
+      for (int j = 0; j < kStageVec; ++j) {
+        const int idx = b0 + threadIdx.x + j * NT;
+        if (idx < n4) {
+          const int t = idx / K4, i = idx - t * K4;
+          vg[j] = gu4[static_cast<int64_t>(t) * 2 * K4 + i];
+          vu[j] = gu4[static_cast<int64_t>(t) * 2 * K4 + K4 + i];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kStageVec; ++j) {
+        const int idx = b0 + threadIdx.x + j * NT;
+        if (idx < n4) {
+          const int t = idx / K4, i = 4 * (idx - t * K4);
+          auto act = [](float g, float u) { return f16_of_product(g / (1.0f + expf(-g)), u); };
+          store_half4(sxb + t * XR + i, act(vg[j].x, vu[j].x), act(vg[j].y, vu[j].y), act(vg[j].z, vu[j].z),
+                             act(vg[j].w, vu[j].w));
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// kRope: each token's position and (k/v tiles) paged-cache row, looked up by one wave while
+// the others run the product (a chain of three dependent loads).
+__device__ __forceinline__ void rope_lookups(const RopeArgs& ra, int tile, int T, int lane, int* s_pos,
+                                             int64_t* s_kvrow) {
+  const int tph = ra.D / 16, h = tile / tph;
+  for (int t = lane; t < T; t += kWave) {
+    const int p = ra.pos[t];
+    s_pos[t] = p;
+    if (h >= ra.heads) {
+      const int block = ra.tables[ra.table_off[ra.seq[t]] + p / ra.block_size];
+      s_kvrow[t] = kv_row_offset(block, ra.kv_heads, (h - ra.heads) % ra.kv_heads, ra.block_size, p % ra.block_size,
+                                 ra.D);
+    }
+  }
+}
+
+// T <= 16 * NB tokens: NB column blocks of 16 tokens share each converted A operand, and
+// RT 16-row tiles share each activation operand (a workgroup covers 16 RT rows: above 16
+// tokens every workgroup re-reads all T activation rows of K through L2, so fewer, taller
+// workgroups read less). Fewer chunks per load batch as NB grows keeps the operands in
+// registers.
+// PRO / EPI as for the fp16 kernel below (fused producer, qkv_post epilogue); a fused
+// instance has NB = RT = 1 and 16-row workgroups, and issues its first batch of weight loads
+// before the prologue.
+template <int WAVES, int NB, int RT, bool F16_SCALE, int PRO = kPlain, int EPI = kStore>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
+                                                                  const void* __restrict__ scale,
+                                                                  const void* __restrict__ xin,
+                                                                  const float* __restrict__ norm_w, float eps,
+                                                                  float* y, int T, int K, int N, float beta,
+                                                                  int rows_per, RopeArgs ra) {
+  static_assert(PRO == kPlain || (NB == 1 && RT == 1), "fused int8 products take one 16-row tile, <= 16 tokens");
+  static_assert(EPI == kStore || PRO != kSiluMul, "the qkv epilogue follows a plain or RMSNorm product");
+  constexpr int U = NB == 1 ? (RT <= 2 ? kUnroll : 2) : (NB == 2 ? 2 : 1);
+  __shared__ float red[WAVES][RT][NB][kWave * 4];
+  __shared__ float s_inv[PRO == kRmsNorm ? kMaxTokens : 1];
+  __shared__ int s_pos[EPI == kRope ? kMaxTokens : 1];
+  __shared__ int64_t s_kvrow[EPI == kRope ? kMaxTokens : 1];
+  extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
+  const half_t* x = static_cast<const half_t*>(xin);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  // Rows [n0, nl) of W: rows_per <= 16 RT rows per workgroup (the last tile may be partly
+  // empty: its rows load nothing and store nothing). kRope: the tile's rows are the RoPE
+  // pairs of rope_tile_row.
+  const int n0 = blockIdx.x * rows_per, nl = min(N, n0 + rows_per);
+  auto out_row = [&](int rt, int m) { return EPI == kRope ? rope_tile_row(blockIdx.x, m, ra.D) : n0 + 16 * rt + m; };
+  const int nchunks = (K + kChunk - 1) / kChunk;
+  const int per = (nchunks + WAVES - 1) / WAVES;
+  const int cb = w * per, ce = min(nchunks, cb + per);
+  const int8_t* wrow[RT];
+  bool rv[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    wrow[rt] = w8 + static_cast<int64_t>(min(out_row(rt, c), N - 1)) * ldw;
+    rv[rt] = EPI == kRope || n0 + 16 * rt + c < nl;
+  }
+  bool tok[NB];
+  const half_t* xrow[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    tok[b] = 16 * b + c < T;
+    xrow[b] = x + static_cast<int64_t>(tok[b] ? 16 * b + c : 0) * K;
+  }
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint4v wv[RT][U];
+  auto load_w = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (q0 + u) * kChunk + 16 * g;
+      const bool live = q0 + u < ce && k < K;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        wv[rt][u] = live && rv[rt] ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
+    }
+  };
+  if (PRO != kPlain) load_w(cb);
+
+  // Wave 0 writes the results. Its row scales (and the old y for beta != 0, where the
+  // registers allow) are loaded before the weights: issued after the reduction they would
+  // queue behind the weight stream (measured 0.7-3.8 us of dependent-load tail).
+  constexpr bool kEarlyY = NB * RT <= 2;
+  float sc[RT][4], yold[RT][NB][4], rbias[4], rfreq[4];
+  if (w == 0) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = min(out_row(rt, 4 * g + r), N - 1);
+        if (F16_SCALE) sc[rt][r] = static_cast<float>(static_cast<const half_t*>(scale)[n]);
+        else sc[rt][r] = static_cast<const float*>(scale)[n];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          yold[rt][b][r] = EPI == kStore && kEarlyY && beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + n] : 0.0f;
+      }
+    if (EPI == kRope) rope_operands(ra, blockIdx.x, g, rbias, rfreq);
+  }
+  constexpr int kVec = WAVES >= 16 && PRO == kRmsNorm ? 4 : 8;
+  if (PRO != kPlain) stage_operands<PRO, WAVES, kVec>(xin, norm_w, eps, T, K, sxb, s_inv);
+  if (EPI == kRope && w == WAVES - 1) rope_lookups(ra, blockIdx.x, T, lane, s_pos, s_kvrow);
+
+  float4v acc[RT][NB];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[rt][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q0 = cb; q0 < ce; q0 += U) {
+    if (PRO == kPlain) load_w(q0);
+    half8 xa[NB][U], xb[NB][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (q0 + u) * kChunk + 16 * g;
+      const bool live = q0 + u < ce && k < K;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (PRO == kPlain) {
+          xa[b][u] = live && tok[b] ? load_half8(xrow[b] + k) : zero;
+          xb[b][u] = live && tok[b] ? load_half8(xrow[b] + k + 8) : zero;
+        } else {
+          // Columns past T read a real row (never written out); chunks past K read nothing.
+          const half_t* xs = sxb + min(16 * b + c, T - 1) * (K + 8) + k;
+          xa[b][u] = live ? *reinterpret_cast<const half8*>(xs) : zero;
+          xb[b][u] = live ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const half8 a0 = int8x8_to_half8(wv[rt][u][0], wv[rt][u][1]);
+        const half8 a1 = int8x8_to_half8(wv[rt][u][2], wv[rt][u][3]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          acc[rt][b] = mfma16x16x32(a0, xa[b][u], acc[rt][b]);
+          acc[rt][b] = mfma16x16x32(a1, xb[b][u], acc[rt][b]);
+        }
+      }
+    if (PRO != kPlain && q0 + U < ce) load_w(q0 + U);
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[w][rt][b][lane * 4 + r] = acc[rt][b][r];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      // Lane (c, g) sums the waves for token 16b + c, rows n0 + 16 rt + 4g + r, in a fixed order.
+      float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] += red[ww][rt][b][lane * 4 + r];
+      if (EPI == kRope) {
+        // The scaled sums as the plain product stores them, then qkv_post's arithmetic.
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = s[r] * sc[rt][r] + 0.0f;
+        const int t = tok[b] ? 16 * b + c : 0;
+        rope_epilogue(ra, v, rbias, rfreq, blockIdx.x, g, 16 * b + c, tok[b], y, N, s_pos[t], s_kvrow[t]);
+        continue;
+      }
+      if (!tok[b]) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = n0 + 16 * rt + 4 * g + r;
+        if (n >= nl) continue;
+        float* dst = y + static_cast<int64_t>(16 * b + c) * N + n;
+        *dst = s[r] * sc[rt][r] + (beta != 0.0f ? beta * (kEarlyY ? yold[rt][b][r] : *dst) : 0.0f);
+      }
+    }
+}
+
 // fp16 weights, T <= 16 * NB tokens (NB column blocks of 16 tokens share each A operand).
 template <int WAVES, int NB, int PRO, int EPI>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* __restrict__ wt, int64_t ldw,
@@ -329,71 +489,8 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
       for (int r = 0; r < 4; ++r)
         yold[b][r] = kEarlyY && beta != 0.0f && tok[b] ? y[static_cast<int64_t>(16 * b + c) * N + min(n0 + 4 * g + r, N - 1)] : 0.0f;
   }
-  if (PRO == kRmsNorm) {
-    const float* xf = static_cast<const float*>(xin);
-    // The staged values' inputs (x and norm_w of this thread's elements) are loaded with the
-    // sums' loads, so the prologue waits for one round of loads instead of three.
-    constexpr int kPre = 4;
-    const bool pre = T * K <= kPre * WAVES * kWave;
-    float px[kPre], pw[kPre];
-    if (pre) {
-#pragma unroll
-      for (int j = 0; j < kPre; ++j) {
-        const int idx = threadIdx.x + j * WAVES * kWave;
-        px[j] = idx < T * K ? xf[idx] : 0.0f;
-        pw[j] = idx < T * K ? norm_w[idx % K] : 0.0f;
-      }
-    }
-    for (int t = w; t < T; t += WAVES) {
-      double ss = 0;
-#pragma unroll 8
-      for (int i = lane; i < K; i += kWave) ss += static_cast<double>(xf[static_cast<int64_t>(t) * K + i]) *
-                                                 xf[static_cast<int64_t>(t) * K + i];
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-      if (lane == 0) s_inv[t] = 1.0f / sqrtf(static_cast<float>(ss / K) + eps);
-    }
-    __syncthreads();
-    if (pre) {
-#pragma unroll
-      for (int j = 0; j < kPre; ++j) {
-        const int idx = threadIdx.x + j * WAVES * kWave;
-        if (idx < T * K) {
-          const int t = idx / K, i = idx - t * K;
-          sxb[t * XR + i] = f16_of_product(pw[j], px[j] * s_inv[t]);
-        }
-      }
-    } else {
-#pragma unroll 4
-      for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
-        const int t = idx / K, i = idx - t * K;
-        sxb[t * XR + i] = f16_of_product(norm_w[i], xf[static_cast<int64_t>(t) * K + i] * s_inv[t]);
-      }
-    }
-    __syncthreads();
-  } else if (PRO == kSiluMul) {
-    const float* gu = static_cast<const float*>(xin);
-#pragma unroll 4
-    for (int idx = threadIdx.x; idx < T * K; idx += WAVES * kWave) {
-      const int t = idx / K, i = idx - t * K;
-      const float v = gu[static_cast<int64_t>(t) * 2 * K + i];
-      sxb[t * XR + i] = f16_of_product(v / (1.0f + expf(-v)), gu[static_cast<int64_t>(t) * 2 * K + K + i]);
-    }
-    __syncthreads();
-  }
-
-  if (EPI == kRope && w == WAVES - 1) {
-    const int tph = ra.D / 16, h = blockIdx.x / tph;
-    for (int t = lane; t < T; t += kWave) {
-      const int p = ra.pos[t];
-      s_pos[t] = p;
-      if (h >= ra.heads) {
-        const int block = ra.tables[ra.table_off[ra.seq[t]] + p / ra.block_size];
-        s_kvrow[t] = kv_row_offset(block, ra.kv_heads, (h - ra.heads) % ra.kv_heads, ra.block_size,
-                                   p % ra.block_size, ra.D);
-      }
-    }
-  }
+  stage_operands<PRO, WAVES, WAVES >= 16 ? 4 : 8>(xin, norm_w, eps, T, K, sxb, s_inv);
+  if (EPI == kRope && w == WAVES - 1) rope_lookups(ra, blockIdx.x, T, lane, s_pos, s_kvrow);
 
   float4v acc[NB];
 #pragma unroll
@@ -514,10 +611,10 @@ int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x,
   const int tiles = (N + rows_per - 1) / rows_per;
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, NB, RT, F16_SCALE>), dim3(tiles), dim3(16 * kWave), 0, s,
-                                     w8, ldw, scale, x, y, T, K, N, beta, rows_per));
+                                     w8, ldw, scale, x, nullptr, 0.0f, y, T, K, N, beta, rows_per, RopeArgs{}));
   } else {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, NB, RT, F16_SCALE>), dim3(tiles), dim3(8 * kWave), 0, s,
-                                     w8, ldw, scale, x, y, T, K, N, beta, rows_per));
+                                     w8, ldw, scale, x, nullptr, 0.0f, y, T, K, N, beta, rows_per, RopeArgs{}));
   }
   return 0;
 }
@@ -569,10 +666,99 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
               : launch_nb<4, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
 }
 
+// The int8 product with a fused producer (PRO) and/or the qkv epilogue (EPI): 16-row
+// workgroups, the wave count of the plain launch for the same N (so the sums are the plain
+// product's, bit for bit).
+template <bool F16_SCALE, int PRO, int EPI>
+int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* xin, const float* norm_w, float eps,
+                 float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
+  const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
+  RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
+  const int tiles = (N + 15) / 16;
+  if (tiles < 256) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(16 * kWave),
+                                     staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16, ra));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(8 * kWave),
+                                     staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16, ra));
+  }
+  return 0;
+}
+
+int check_int8_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x, int T, int K, int N) {
+  RH_REQUIRE(T >= 1 && T <= kMaxTokens, "gemv_int8 fused: T must be in 1..16");
+  RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemv_int8: ldw must be >= K and a multiple of 16");
+  RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr, "gemv_int8: missing pointer");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemv_int8: W8 and x must be 16-byte aligned");
+  return 0;
+}
+
+int check_rope(const float* inv_freq, const int* pos, const int* seq, const int* table_off, const int* tables,
+               void* kpool, void* vpool, int heads, int kv_heads, int head_dim, int block_size) {
+  RH_REQUIRE(inv_freq && pos && seq && table_off && tables && kpool && vpool, "qkv epilogue: missing pointer");
+  RH_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "qkv epilogue: bad head counts");
+  RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "qkv epilogue: head_dim must be a multiple of 16");
+  RH_REQUIRE(block_size > 0, "qkv epilogue: bad block size");
+  return 0;
+}
+
+template <int PRO, int EPI>
+int int8_fused(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* xin,
+               const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream,
+               const RopeArgs& ra = RopeArgs{}) {
+  if (int rc = check_int8_fused(w8, ldw, scale, xin, T, K, N)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return scale_is_f16 ? launch_fused<true, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra)
+                      : launch_fused<false, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra);
+}
+
 }  // namespace
 }  // namespace relay_hip
 
 using namespace relay_hip;
+
+extern "C" int rh_gemv_int8_rmsnorm(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
+                                    const float* norm_w, float eps, float* y, int T, int K, int N, float beta,
+                                    void* stream) {
+  RH_REQUIRE(norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 == 0,
+             "gemv_int8_rmsnorm: norm weights missing or not 16-byte aligned");
+  return int8_fused<kRmsNorm, kStore>(w8, ldw, scale, scale_is_f16, x, norm_w, eps, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* gu,
+                                 float* y, int T, int K, int N, float beta, void* stream) {
+  return int8_fused<kSiluMul, kStore>(w8, ldw, scale, scale_is_f16, gu, nullptr, 0.0f, y, T, K, N, beta, stream);
+}
+
+extern "C" int rh_gemv_int8_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
+                                float* qkv, int T, int K, const float* bias, const float* inv_freq, const int* pos,
+                                const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
+                                void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+  if (int rc = check_rope(inv_freq, pos, seq, table_off, tables, kpool, vpool, heads, kv_heads, head_dim, block_size))
+    return rc;
+  RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
+              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  return int8_fused<kPlain, kRope>(w8, ldw, scale, scale_is_f16, x, nullptr, 0.0f, qkv, T, K, N, 0.0f, stream, ra);
+}
+
+extern "C" int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16,
+                                        const float* x, const float* norm_w, float eps, float* qkv, int T, int K,
+                                        const float* bias, const float* inv_freq, const int* pos, const int* seq,
+                                        const int* table_off, const int* tables, void* kpool, void* vpool,
+                                        void* q_out, int heads, int kv_heads, int head_dim, int block_size,
+                                        void* stream) {
+  RH_REQUIRE(norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 == 0,
+             "gemv_int8_rmsnorm_qkv: norm weights missing or not 16-byte aligned");
+  if (int rc = check_rope(inv_freq, pos, seq, table_off, tables, kpool, vpool, heads, kv_heads, head_dim, block_size))
+    return rc;
+  RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
+              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  return int8_fused<kRmsNorm, kRope>(w8, ldw, scale, scale_is_f16, x, norm_w, eps, qkv, T, K, N, 0.0f, stream, ra);
+}
 
 extern "C" int rh_gemv_int8_max_tokens(void) { return kMaxInt8Tokens; }
 
@@ -658,7 +844,8 @@ extern "C" int rh_gemv_f16_splitk(const void* w16, int64_t ldw, const void* x, f
 
 extern "C" int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
                                    float* y, int T, int K, int N, float beta, void* stream) {
-  RH_REQUIRE(norm_w != nullptr, "gemv_f16_rmsnorm: no norm weights");
+  RH_REQUIRE(norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 == 0,
+             "gemv_f16_rmsnorm: norm weights missing or not 16-byte aligned");
   return gemv_f16_launch<kRmsNorm>(w16, ldw, x, norm_w, eps, y, T, K, N, beta, stream);
 }
 
@@ -688,6 +875,7 @@ extern "C" int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float
                                        int block_size, void* stream) {
   RH_REQUIRE(norm_w != nullptr && inv_freq && pos && seq && table_off && tables && kpool && vpool,
              "gemv_f16_rmsnorm_qkv: missing pointer");
+  RH_REQUIRE(reinterpret_cast<uintptr_t>(norm_w) % 16 == 0, "gemv_f16_rmsnorm_qkv: norm weights not 16-byte aligned");
   RH_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gemv_f16_rmsnorm_qkv: bad head counts");
   RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "gemv_f16_rmsnorm_qkv: head_dim must be a multiple of 16");
   RH_REQUIRE(block_size > 0, "gemv_f16_rmsnorm_qkv: bad block size");

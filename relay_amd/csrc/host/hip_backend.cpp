@@ -205,7 +205,8 @@ class HipBackend final : public Backend {
   DeviceArray<float> make_f32(const float* host, std::size_t n, float fill);
   void upload_f32_rows(const float* host, int N, int K, const std::function<void(const float*, int, int)>& apply);
   void gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta);
-  bool fused(const DeviceMatrix& W, int T) const;
+  // int8_ok: the caller has an int8 variant of the fused product (the qkv projection).
+  bool fused(const DeviceMatrix& W, int T, bool int8_ok = false) const;
   void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
   // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
   static bool skinny(int K, int N, int T);
@@ -396,13 +397,17 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
 
 bool HipBackend::skinny(int K, int N, int T) { return K % 16 == 0 && T <= 16; }
 
-bool HipBackend::fused(const DeviceMatrix& W, int T) const {
+bool HipBackend::fused(const DeviceMatrix& W, int T, bool int8_ok) const {
   // Normalisation / activation folded into the skinny fp16 product, up to 16 tokens, when its
   // 16-row tiles fit one round of workgroups on the CUs: every workgroup repeats the
   // prologue, so on wider matrices the repeats cost more than the launch they save (TinyLlama
   // gate_up, 704 tiles, at T = 8: 27.7 us fused against 3.7 + 13.8 us for RMSNorm and the
-  // library product).
-  return !W.i8.p && T <= 16 && W.K % 16 == 0 && (W.N + 15) / 16 <= 256 && rh_gemv_f16_fused_fits(T, W.K);
+  // library product). With int8 weights only the qkv projection takes its RMSNorm and
+  // qkv_post (TinyLlama int8 decode steps, ms: b = 1 1.073 -> 1.042, b = 4 1.169 -> 1.141);
+  // the SiLU prologue on the int8 down projection was no faster at b = 1, 8, 16 and slower at
+  // b = 4 (1.169 -> 1.240), gate_up never has few enough tiles.
+  return (!W.i8.p || int8_ok) && T <= 16 && W.K % 16 == 0 && (W.N + 15) / 16 <= 256 &&
+         rh_gemv_f16_fused_fits(T, W.K);
 }
 
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
@@ -563,11 +568,23 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
     std::uint16_t* vc = vc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
     const float* bias = L.bqkv.n ? L.bqkv.p : nullptr;
     std::uint16_t* q_out = fast_attention_ ? qh_.p : nullptr;
-    if (fused(L.wqkv, T) && D % 16 == 0) {
+    if (fused(L.wqkv, T, true) && D % 16 == 0) {
       // RMSNorm, the projection and qkv_post in one launch.
-      RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
-                                       d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
-                                       layout_.block_size, stream_));
+      if (L.wqkv.i8.p)
+        RH_CHECK(rh_gemv_int8_rmsnorm_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, x_.p, L.attn_norm.p, eps, qkv_.p,
+                                          T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out,
+                                          c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+      else
+        RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
+                                         d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
+                                         layout_.block_size, stream_));
+    } else if (L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 && T <= 16 && (QKV + 15) / 16 <= 256) {
+      // int8: the projection and qkv_post in one launch (its 16-row tiles in one round;
+      // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms).
+      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      RH_CHECK(rh_gemv_int8_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, xn_.p, qkv_.p, T, H, bias, inv_freq_.p,
+                                d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
+                                layout_.block_size, stream_));
     } else if (!L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 &&
                (T <= 16 || (T <= rh_gemv_f16_max_tokens() && QKV <= 4096)) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
       // (17-32 tokens: TinyLlama's 2560-row qkv 11.1 us here against 9.5 + 3.0 us for the

@@ -126,3 +126,145 @@ def test_rejects_bad_shapes(torch_mod, dev):
     assert _lib.lib().rh_gemv_int8(None, 72, None, 0, None, None, 1, 72, 64, 0.0, None) != 0
     assert _lib.lib().rh_gemv_int8(None, 48, None, 0, None, None, 1, 64, 64, 0.0, None) != 0
     assert "ldw" in _lib.last_error()
+
+
+# Fused producers and the qkv epilogue on the int8 GEMV: the same bits as the launches they
+# replace (rh_rmsnorm / rh_silu_mul, rh_gemv_int8, rh_qkv_post), whose parts are checked
+# against their own references (test_layer_ops.py and the tests above), wherever the two use
+# the same wave split of K (every shape with at most 256 16-row tiles, the backend's use);
+# against the float64 oracle elsewhere.
+def _fused_vs_chain(torch, dev, kind, T, K, N, beta, f16_scale, seed):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    rng = np.random.default_rng(seed)
+    w8 = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    scale = rng.uniform(0.001, 0.02, size=N).astype(np.float32)
+    ldw = L.rh_gemv_int8_row_stride(K)
+    padded = np.full((N, ldw), 0x7F, np.int8)
+    padded[:, :K] = w8
+    W = torch.from_numpy(padded).to(dev)
+    S = torch.from_numpy(f16_bits(scale).view(np.int16) if f16_scale else scale).to(dev)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    want = torch.from_numpy(y0.copy()).to(dev)
+    got = torch.from_numpy(y0.copy()).to(dev)
+    xh = torch.empty((T, K), dtype=torch.int16, device=dev)
+    print(f"gemv_int8 fused {kind}: T={T} K={K} N={N} beta={beta} f16_scale={f16_scale}", flush=True)
+    if kind == "rmsnorm":
+        x = torch.from_numpy((rng.standard_normal((T, K)) * 3).astype(np.float32)).to(dev)
+        nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).to(dev)
+        _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), K, 1e-5, xh.data_ptr(), None), "rh_rmsnorm")
+        _lib.check(L.rh_gemv_int8_rmsnorm(W.data_ptr(), ldw, S.data_ptr(), int(f16_scale), x.data_ptr(), nw.data_ptr(),
+                                          1e-5, got.data_ptr(), T, K, N, beta, None), "rh_gemv_int8_rmsnorm")
+    else:
+        gu = torch.from_numpy((rng.standard_normal((T, 2 * K)) * 2).astype(np.float32)).to(dev)
+        _lib.check(L.rh_silu_mul(gu.data_ptr(), T, K, xh.data_ptr(), None), "rh_silu_mul")
+        _lib.check(L.rh_gemv_int8_silu(W.data_ptr(), ldw, S.data_ptr(), int(f16_scale), gu.data_ptr(), got.data_ptr(),
+                                       T, K, N, beta, None), "rh_gemv_int8_silu")
+    _lib.check(L.rh_gemv_int8(W.data_ptr(), ldw, S.data_ptr(), int(f16_scale), xh.data_ptr(), want.data_ptr(), T, K, N,
+                              beta, None), "rh_gemv_int8")
+    torch.cuda.synchronize()
+    s_used = bits_to_f32(f16_bits(scale)) if f16_scale else scale
+    return want.cpu().numpy(), got.cpu().numpy(), (w8, s_used, xh.cpu().numpy().view(np.uint16), y0)
+
+
+@pytest.mark.parametrize("kind", ["rmsnorm", "silu"])
+@pytest.mark.parametrize("T,K,N,beta,f16_scale", [(1, 576, 960, 0.0, False), (16, 576, 3072, 0.0, True),
+                                                  (7, 1536, 576, 1.0, False), (3, 4096, 512, 1.0, True),
+                                                  (2, 14336, 256, 1.0, False), (5, 5632, 2048, 1.0, True),
+                                                  (16, 2032, 4096, 0.0, False), (9, 48, 33, 0.0, False),
+                                                  (4, 2048, 4104, 0.0, True)])
+def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta, f16_scale):
+    want, got, _ = _fused_vs_chain(torch_mod, dev, kind, T, K, N, beta, f16_scale, seed=T + K + N)
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["rmsnorm", "silu"])
+def test_fused_producers_on_wide_matrices(torch_mod, dev, kind):
+    """6144 rows at T = 8: the plain launch takes two row tiles per workgroup (16 waves), the
+    fused one 16-row workgroups (8 waves), so the sums differ in order: both within the
+    fp32-accumulation bound of the float64 product of the same fp16 operands."""
+    T, K, N = 8, 1024, 6144
+    want, got, (w8, s, xb, y0) = _fused_vs_chain(torch_mod, dev, kind, T, K, N, 1.0, False, seed=7)
+    exact = O.gemv_int8(w8, s, xb, beta=1.0, y0=y0)
+    tol = bound(w8, s, xb) + 2 * EPS32 * np.abs(exact)
+    assert (np.abs(got - exact) <= tol).all() and (np.abs(want - exact) <= tol).all()
+
+
+def test_fused_limits(torch_mod, dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_int8_silu(None, 2048, None, 0, None, None, 16, 2048, 64, 0.0, None) != 0
+    assert L.rh_gemv_int8_rmsnorm(None, 64, None, 0, None, None, 1e-5, None, 17, 64, 64, 0.0, None) != 0
+
+
+@pytest.mark.parametrize("T,heads,kvh,D,H,bs,with_bias,norm", [
+    (1, 9, 3, 64, 576, 16, False, True), (15, 32, 4, 64, 2048, 16, True, False), (5, 16, 8, 128, 4096, 16, False, True),
+    (8, 8, 2, 64, 320, 12, True, True), (3, 4, 4, 16, 64, 1, True, True), (16, 32, 4, 64, 2048, 16, False, False),
+    (2, 16, 4, 128, 2048, 16, False, False)])
+def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias, norm):
+    """rh_gemv_int8_rmsnorm_qkv (norm) or rh_gemv_int8_qkv (x already normalised) against
+    rh_rmsnorm -> rh_gemv_int8 -> rh_qkv_post. Without rotation (inv_freq = 0) every byte of
+    qkv, q and both caches is equal. With RoPE the inlined sincosf/products of the two kernels
+    round differently in the last bit, so rotated fp32 values must agree within 4 ulp of the
+    pair's magnitude and fp16 values within 1 ulp."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(T * 37 + D + H)
+    N = (heads + 2 * kvh) * D
+    pos = [int(p) for p in rng.permutation(5 * bs + 3)[:T]]  # distinct: one writer per cache slot
+    seq = [t % 2 for t in range(T)]
+    per = (5 * bs + 3) // bs + 1
+    nblocks = 2 * per + 3
+    tables = [int(b) for b in rng.permutation(nblocks)[:2 * per]]
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ldw = L.rh_gemv_int8_row_stride(H)
+    w8 = np.full((N, ldw), 0x7F, np.int8)
+    w8[:, :H] = rng.integers(-127, 128, size=(N, H), dtype=np.int8)
+    W = dt(w8)
+    S = dt(rng.uniform(0.001, 0.02, size=N).astype(np.float32))
+    x = dt((rng.standard_normal((T, H)) * 2).astype(np.float32))
+    nw = dt(rng.uniform(0.5, 1.5, H).astype(np.float32))
+    bias = dt(rng.standard_normal(N).astype(np.float32)) if with_bias else None
+    P, Sq = dt(np.array(pos, np.int32)), dt(np.array(seq, np.int32))
+    TO, TB = dt(np.array([0, per], np.int32)), dt(np.array(tables, np.int32))
+    bp = bias.data_ptr() if bias is not None else None
+
+    def run_qkv(fused, inv):
+        kc = torch.full((nblocks * kvh * bs * D,), 0x7BFF, dtype=torch.int16, device=dev)
+        vc = kc.clone()
+        qo = torch.zeros(T * heads * D, dtype=torch.int16, device=dev)
+        qkv = torch.full((T, N), float("nan"), device=dev)
+        xn = torch.empty((T, H), dtype=torch.int16, device=dev)
+        _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
+        rope = (bp, inv.data_ptr(), P.data_ptr(), Sq.data_ptr(), TO.data_ptr(), TB.data_ptr(), kc.data_ptr(),
+                vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs, None)
+        if fused and not norm:
+            _lib.check(L.rh_gemv_int8_qkv(W.data_ptr(), ldw, S.data_ptr(), 0, xn.data_ptr(), qkv.data_ptr(), T, H, *rope),
+                       "rh_gemv_int8_qkv")
+        elif fused:
+            _lib.check(L.rh_gemv_int8_rmsnorm_qkv(W.data_ptr(), ldw, S.data_ptr(), 0, x.data_ptr(), nw.data_ptr(), 1e-5,
+                                                  qkv.data_ptr(), T, H, *rope), "rh_gemv_int8_rmsnorm_qkv")
+        else:
+            _lib.check(L.rh_gemv_int8(W.data_ptr(), ldw, S.data_ptr(), 0, xn.data_ptr(), qkv.data_ptr(), T, H, N, 0.0,
+                                      None), "rh_gemv_int8")
+            _lib.check(L.rh_qkv_post(qkv.data_ptr(), T, *rope), "rh_qkv_post")
+        torch.cuda.synchronize()
+        return [a.cpu().numpy() for a in (qkv, kc, vc, qo)]
+
+    print(f"int8 fused qkv: T={T} heads={heads}/{kvh} D={D} H={H} bs={bs} bias={with_bias} norm={norm}", flush=True)
+    assert (N + 15) // 16 <= 256 and (not norm or L.rh_gemv_f16_fused_fits(T, H))
+    inv0 = dt(np.zeros(D // 2, np.float32))
+    for name, a, b in zip(("qkv", "k cache", "v cache", "q"), run_qkv(False, inv0), run_qkv(True, inv0)):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+    inv = dt((1.0 / 10000.0 ** (np.arange(0, D, 2) / D)).astype(np.float32))
+    (qa, ka, va, oa), (qb, kb, vb, ob) = run_qkv(False, inv), run_qkv(True, inv)
+    pair = np.abs(qa.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True)
+    bound_q = 4 * 2.0 ** -24 * np.broadcast_to(pair, (T, N // D, 2, D // 2)).reshape(T, N)
+    assert (np.abs(qa - qb) <= bound_q).all()
+    for name, a, b in (("k cache", ka, kb), ("v cache", va, vb), ("q", oa, ob)):
+        diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
+        assert diff.max() <= 1 and (np.sign(a) == np.sign(b)).all(), name
