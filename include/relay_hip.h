@@ -140,8 +140,8 @@ int rh_reference_attention(const float* q, int64_t q_row_stride, const void* kpo
 /* ---- weight-only int8 ----------------------------------------------------------- */
 
 /* y[t, n] = scale[n] * sum_k W8[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for
- * 1 <= T <= 64 tokens (relay's GEMV takes up to 8). W8 int8 [N, K] rows ldw bytes apart (ldw >= K, a multiple of 16;
- * relay's layout is ldw = K); x fp16 [T, K]; y fp32 [T, N].
+ * 1 <= T <= 64 tokens (relay's GEMV takes up to 8). W8 int8 [N, K] rows ldw bytes apart
+ * (K <= ldw < 2^21, a multiple of 16; relay's layout is ldw = K); x fp16 [T, K]; y fp32 [T, N].
  * scale is fp32 [N] (scale_is_f16 = 0, relay's quantizer) or fp16 [N] (scale_is_f16 = 1).
  * K must be a multiple of 16 and W8 / x 16-byte aligned.
  * Replaces gemv_int8_kernel<8> (cuda_kernels.cuh:378-430) and its dispatch

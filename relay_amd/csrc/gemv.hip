@@ -45,6 +45,13 @@ constexpr size_t kFusedLdsBytes = 64 << 10;  // staged activations of the fused 
 constexpr int kChunk = 64;   // k per wave step
 constexpr int kUnroll = 4;   // chunks whose loads are issued together
 
+// int8 weight rows are read through a buffer resource based at the workgroup's first row
+// (32-bit offsets from a scalar base instead of 64-bit addresses: measured 1-3% faster at
+// T = 1-4 on the Llama-3 shapes; level for the fp16 kernel, which keeps global loads).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
 __device__ __forceinline__ half8 int8x8_to_half8(uint32_t lo, uint32_t hi) {
   // bytes b -> halves with bits 0x6400 | (b ^ 0x80), minus 1152.
   const uint32_t x0 = lo ^ 0x80808080u, x1 = hi ^ 0x80808080u;
@@ -299,11 +306,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   const int nchunks = (K + kChunk - 1) / kChunk;
   const int per = (nchunks + WAVES - 1) / WAVES;
   const int cb = w * per, ce = min(nchunks, cb + per);
-  const int8_t* wrow[RT];
+  // Rows of this workgroup lie in [row0, row0 + 16 RT) (kRope: within one head's D rows).
+  const int row0 = EPI == kRope ? (blockIdx.x / (ra.D / 16)) * ra.D : n0;
+  const __amdgpu_buffer_rsrc_t wrs = weight_rsrc(w8 + static_cast<int64_t>(row0) * ldw);
+  int woff[RT];
   bool rv[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    wrow[rt] = w8 + static_cast<int64_t>(min(out_row(rt, c), N - 1)) * ldw;
+    woff[rt] = (min(out_row(rt, c), N - 1) - row0) * static_cast<int>(ldw);
     rv[rt] = EPI == kRope || n0 + 16 * rt + c < nl;
   }
   bool tok[NB];
@@ -322,7 +332,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
       const bool live = q0 + u < ce && k < K;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
-        wv[rt][u] = live && rv[rt] ? *reinterpret_cast<const uint4v*>(wrow[rt] + k) : uint4v{0u, 0u, 0u, 0u};
+        wv[rt][u] = live && rv[rt] ? __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[rt] + k, 0, 0) : uint4v{0u, 0u, 0u, 0u};
     }
   };
   if (PRO != kPlain) load_w(cb);
@@ -688,7 +698,8 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
 int check_int8_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x, int T, int K, int N) {
   RH_REQUIRE(T >= 1 && T <= kMaxTokens, "gemv_int8 fused: T must be in 1..16");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
-  RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemv_int8: ldw must be >= K and a multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
+             "gemv_int8: ldw must be >= K, < 2^21 and a multiple of 16");
   RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr, "gemv_int8: missing pointer");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_int8: W8 and x must be 16-byte aligned");
@@ -772,7 +783,8 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
                             float* y, int T, int K, int N, float beta, void* stream) {
   RH_REQUIRE(T >= 1 && T <= kMaxInt8Tokens, "gemv_int8: T must be in 1..64");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
-  RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemv_int8: ldw must be >= K and a multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
+             "gemv_int8: ldw must be >= K, < 2^21 and a multiple of 16");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_int8: W8 and x must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);

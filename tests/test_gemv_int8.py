@@ -126,6 +126,9 @@ def test_rejects_bad_shapes(torch_mod, dev):
     assert _lib.lib().rh_gemv_int8(None, 72, None, 0, None, None, 1, 72, 64, 0.0, None) != 0
     assert _lib.lib().rh_gemv_int8(None, 48, None, 0, None, None, 1, 64, 64, 0.0, None) != 0
     assert "ldw" in _lib.last_error()
+    # rows are addressed with 32-bit offsets from the workgroup's first row
+    assert _lib.lib().rh_gemv_int8(None, 1 << 21, None, 0, None, None, 1, 64, 64, 0.0, None) != 0
+    assert "2^21" in _lib.last_error()
 
 
 # Fused producers and the qkv epilogue on the int8 GEMV: the same bits as the launches they
