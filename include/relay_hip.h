@@ -108,6 +108,10 @@ int rh_decode_slice_keys(int n_dec, int kv_heads, int group, int head_dim, int m
  *              two blocks of rows (first row, rows, first position) and the chunk's
  *              block-table offset
  *  tables      the block tables the records' offsets point into
+ *  scale       scores are scale * q.k; the kernel works in the exp2 domain and rounds
+ *              q * scale * log2(e) to fp16 once more, unless that multiplier is exactly 1
+ *              (scale = ln 2): then q is taken as already scaled, as the q writers'
+ *              q_scale leaves it (the backend's path)
  * head_dim in {16, 32, 64, 128} (16 computed at width 32). */
 int rh_flash_prefill(const void* q, int64_t q_row_stride, const void* kpool, const void* vpool, const int* tables,
                      const int* work, int n_work, int heads, int kv_heads, int head_dim, int block_size, float scale,
@@ -170,13 +174,13 @@ int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scale, int scal
                       int T, int K, int N, float beta, void* stream);
 int rh_gemv_int8_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x, float* qkv,
                      int T, int K, const float* bias, const float* inv_freq, const int* pos, const int* seq,
-                     const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
-                     int kv_heads, int head_dim, int block_size, void* stream);
+                     const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, float q_scale,
+                     int heads, int kv_heads, int head_dim, int block_size, void* stream);
 int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
                              const float* norm_w, float eps, float* qkv, int T, int K, const float* bias,
                              const float* inv_freq, const int* pos, const int* seq, const int* table_off,
-                             const int* tables, void* kpool, void* vpool, void* q_out, int heads, int kv_heads,
-                             int head_dim, int block_size, void* stream);
+                             const int* tables, void* kpool, void* vpool, void* q_out, float q_scale, int heads,
+                             int kv_heads, int head_dim, int block_size, void* stream);
 
 /* y[t, n] = sum_k W16[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for 1 <= T <= 32:
  * the dense projection at decode batch sizes. W16 fp16 [N, K] rows ldw elements apart
@@ -220,15 +224,16 @@ int rh_gemv_f16_fused_fits(int T, int K);
 int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
                             float* qkv, int T, int K, const float* bias, const float* inv_freq, const int* pos,
                             const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
-                            void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream);
+                            void* q_out, float q_scale, int heads, int kv_heads, int head_dim, int block_size,
+                            void* stream);
 
 /* The same with x already fp16 [T, K] (no normalisation): rh_gemv_f16 then rh_qkv_post in
  * one launch, for the token counts where the RMSNorm cannot be folded in (1 <= T <= 32).
  * No counterpart in relay (cuda_backend.cu:577-578 are two launches). */
 int rh_gemv_f16_qkv(const void* w16, int64_t ldw, const void* x, float* qkv, int T, int K, const float* bias,
                     const float* inv_freq, const int* pos, const int* seq, const int* table_off, const int* tables,
-                    void* kpool, void* vpool, void* q_out, int heads, int kv_heads, int head_dim, int block_size,
-                    void* stream);
+                    void* kpool, void* vpool, void* q_out, float q_scale, int heads, int kv_heads, int head_dim,
+                    int block_size, void* stream);
 
 /* Largest T rh_gemv_f16 takes. */
 int rh_gemv_f16_max_tokens(void);
@@ -281,10 +286,13 @@ int rh_rmsnorm(const float* x, const int* rows, int R, const float* w, int H, fl
 
 /* Per token: qkv row += bias (if not NULL); RoPE on the q and k heads (pairs (i, i + D/2),
  * angle pos * inv_freq[i]); k and v written as fp16 into the paged cache; q written as
- * fp16 to q_out (row stride heads * head_dim). (cuda_backend.cu:171-198) */
+ * fp16(q * q_scale) to q_out (row stride heads * head_dim; may be NULL). q_scale = 1 is the
+ * plain copy; the backend passes softmax scale * log2(e), so that the attention kernels get
+ * queries already in their exp2 domain with one rounding (and are called with scale = ln 2).
+ * Every q_out writer below takes q_scale the same way. (cuda_backend.cu:171-198) */
 int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, const int* pos, const int* seq,
-                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
-                int kv_heads, int head_dim, int block_size, void* stream);
+                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, float q_scale,
+                int heads, int kv_heads, int head_dim, int block_size, void* stream);
 
 /* rh_qkv_post without the fp32 write-back: the same q (fp16, to q_out, required) and cache
  * rows, qkv left as it is. For callers that read only q_out and the cache afterwards (the
@@ -293,7 +301,8 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
  * place, cuda_backend.cu:171-198). */
 int rh_qkv_post_to_cache(const float* qkv, int T, const float* bias, const float* inv_freq, const int* pos,
                          const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
-                         void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream);
+                         void* q_out, float q_scale, int heads, int kv_heads, int head_dim, int block_size,
+                         void* stream);
 
 /* act[t, i] = fp16(g * sigmoid(g) * u), g = gu[t, i], u = gu[t, I + i]. (cuda_backend.cu:245-253) */
 int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream);

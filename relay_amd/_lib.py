@@ -60,8 +60,8 @@ SIGNATURES = {
     "rh_gemv_int8": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
     "rh_gemv_int8_rmsnorm": (I, [P, I64, P, I, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_int8_silu": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
-    "rh_gemv_int8_qkv": (I, [P, I64, P, I, P, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
-    "rh_gemv_int8_rmsnorm_qkv": (I, [P, I64, P, I, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_gemv_int8_qkv": (I, [P, I64, P, I, P, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
+    "rh_gemv_int8_rmsnorm_qkv": (I, [P, I64, P, I, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
     "rh_gemv_int8_row_stride": (I64, [I]),
     "rh_gemv_f16": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_splitk": (I, [P, I64, P, P, I, I, I, F, I, P, P, P]),
@@ -73,16 +73,16 @@ SIGNATURES = {
     "rh_gemv_f16_rmsnorm": (I, [P, I64, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_f16_silu": (I, [P, I64, P, P, I, I, I, F, P]),
     "rh_gemv_f16_fused_fits": (I, [I, I]),
-    "rh_gemv_f16_rmsnorm_qkv": (I, [P, I64, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
-    "rh_gemv_f16_qkv": (I, [P, I64, P, P, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_gemv_f16_rmsnorm_qkv": (I, [P, I64, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
+    "rh_gemv_f16_qkv": (I, [P, I64, P, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
     "rh_gemv_int8_max_tokens": (I, []),
     "rh_quantize_int8": (I, [P, I, I, P, I64, P, P]),
     "rh_dequant_int8": (I, [P, I64, P, I, I, P, P]),
     "rh_f32_to_f16": (I, [P, P, SZ, P]),
     "rh_embed": (I, [P, I, P, I, P, P]),
     "rh_rmsnorm": (I, [P, P, I, P, I, F, P, P]),
-    "rh_qkv_post": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
-    "rh_qkv_post_to_cache": (I, [P, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P]),
+    "rh_qkv_post": (I, [P, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
+    "rh_qkv_post_to_cache": (I, [P, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
     "rh_silu_mul": (I, [P, I, I, P, P]),
     "rh_kv_gather": (I, [P, P, P, I, SZ, P, P]),
     "rh_kv_scatter": (I, [P, P, P, I, SZ, P, P]),

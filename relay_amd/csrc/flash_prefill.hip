@@ -9,19 +9,23 @@
 //   block of up to 128 consecutive rows of one chunk, or a pair of blocks (i, n-1-i) of
 //   the same chunk processed one after the other, so that every workgroup does the same
 //   causal work (rh_prefill_plan makes the items; it pairs when the grid is large).
-// - Waves 2r and 2r+1 own the block's rows 32r .. 32r+31 and split every key tile (128
-//   keys at head_dim 64, 64 at 128): the first half goes to the even wave, the second to
-//   the odd one. Each keeps its own running max, sum and O^T; at the end of the block the
-//   odd wave hands them to the even one through LDS. So two waves stay busy on every SIMD until the block's last tile (with one wave
-//   per 32-row strip, every SIMD drops to one wave once the short blocks finish).
+// - Waves r and r+4 (the two waves of one SIMD) own the block's rows 32r .. 32r+31 and
+//   split every key tile (128 keys at head_dim 64, 64 at 128): the first half goes to wave
+//   r, the second to wave r+4. Each keeps its own running offset, sum and O^T; at the end of
+//   the block wave r+4 hands them to wave r through LDS. So two waves stay busy on every SIMD
+//   until the block's last tile (with one wave per 32-row strip, every SIMD drops to one wave
+//   once the short blocks finish), and each SIMD holds one wave of each half (the second
+//   halves carry more of the diagonal's work).
 // - The workgroup walks the keys 0 .. (block's last position) a tile at a time: each tile
 //   of K and V is gathered through the block table into registers one tile ahead (its block
 //   ids another tile ahead) and written to one of two LDS buffers (one barrier per tile).
 // - Per wave and half tile (one or two 32-key sub-steps, whose S^T chains interleave):
-//     S^T[32 keys x 32 rows] = K[32 keys x D] * Q^T[D x 32 rows]        (D/16 MFMA 32x32x16)
-//     online softmax per row (lane = row): reductions over the lane's 16 registers plus
-//     one swap with lane l^32; scale and log2(e) folded into one FMA per score; the row
-//     sum from the fp16 P values with packed dot products
+//     S^T[32 keys x 32 rows] = K[32 keys x D] * Q^T[D x 32 rows] - ref  (D/16 MFMA 32x32x16)
+//   with q scaled into the exp2 domain (softmax scale * log2 e) and the accumulators
+//   starting at minus the row's reference offset, so P = exp2(S^T) as it stands; a tile is
+//   accepted while no lane's row sum passes 2^15 (no fp16 overflow) and otherwise redone
+//   with the row maximum (new offset, O^T and sum rescaled) — a few tiles per row. Row sums
+//   from the fp16 P values with packed dot products;
 //     O^T[D x 32 rows] += V^T[D x 16 keys] * P^T[16 keys x 32 rows]     (D/32 MFMA 32x32x16)
 //   The S^T accumulators are the P^T B operands as they stand. Lane (c, h) of S^T holds
 //   keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key group: two runs of 4 consecutive keys,
@@ -73,12 +77,27 @@ struct PrefillArgs {
   int64_t out_stride;
 };
 
-// 16-byte chunk swizzle of K and V rows by key. At D128 keys 8 apart also get different
-// chunks (bank conflicts halved, 56.3 -> 55.0 us at 2048 tokens); at D64 the same change
-// measured slower (32.4 -> 34.0 us), so it keeps key & 7.
+// The value of lane l ^ 32 combined with lane l's, through one permlane32 swap (no LDS).
+__device__ __forceinline__ float xlane_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xlane_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]) - x;
+}
+
+// 16-byte chunk swizzle of K and V rows by key, chosen so that none of the kernel's LDS
+// accesses has a bank conflict (64 banks of 4 bytes; a 16-byte access serves 16 lanes per
+// cycle, an 8-byte one 32): the 16 lanes of a K operand read (keys c .. c+15 at one chunk)
+// and the transposing V reads (4 consecutive keys x 4 chunks) each cover every bank once.
+// Measured per instruction against key & 7 (key ^ key >> 3 at 128): K reads 8.2 -> 6.4
+// clocks (16 -> 6.4 at head size 32), V reads at 128 8.0 -> 5.2; 2048-token prefill at
+// head size 128 54.4 -> 52.6 us. Head size 64 keeps key & 7 (K reads 2-way conflicted):
+// the conflict-free (key >> 1) & 7 measured 31.1 -> 31.8 us there.
 template <int D>
 __device__ __forceinline__ int kswz(int key) {
-  return D == 128 ? (key ^ ((key >> 3) & 3)) & 7 : D == 64 ? key & 7 : key & 3;  // within the D / 8 chunks
+  return D == 128 ? ((key & 3) << 2) | ((key >> 2) & 3) : D == 64 ? key & 7 : (key >> 2) & 3;
 }
 
 // D is the compute width, DR the head size of the cache rows, q and out: equal, except head
@@ -106,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
 
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31, hh = lane >> 5;
-  const int strip = w >> 1, half = w & 1;
+  const int strip = w & 3, half = w >> 2;
 
   // Workgroup -> (work item, head).
   const int b = blockIdx.x;
@@ -129,11 +148,13 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
   // Block-table lookups and K/V rows in flight for the tile after the one in LDS.
   int blk[LOADS];
   half8 kreg[LOADS], vreg[LOADS];
-  // Row i of this thread: key 2p + (i & 1) of the tile, 16-byte chunk cc (valid if < ITEMS).
+  // Row i of this thread: key p + (i & 1) * (tile / 2) of the tile, 16-byte chunk cc (valid
+  // if < ITEMS); one load or LDS store instruction covers consecutive keys, i.e. both halves
+  // of the LDS banks (a key row is 128 bytes at head size 64).
   auto item = [&](int i, int& kl, int& cc) {
     const int qi = threadIdx.x + (i >> 1) * kThreads;
     cc = qi % CH;
-    kl = 2 * (qi / CH) + (i & 1);
+    kl = qi / CH + (i & 1) * (ITEMS / CH);
     return ITEMS % kThreads == 0 || qi < ITEMS;
   };
 
@@ -178,26 +199,28 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
     };
     auto store = [&](int buf) {
 #pragma unroll
-      for (int j = 0; j < PAIRS; ++j) {
+      for (int i = 0; i < LOADS; ++i) {
         int kl, cc;
-        if (item(2 * j, kl, cc)) {
-          half_t* kb = sK + buf * KBUF;
-          *reinterpret_cast<half8*>(kb + kl * D + ((cc ^ kswz<D>(kl)) << 3)) = kreg[2 * j];
-          *reinterpret_cast<half8*>(kb + (kl + 1) * D + ((cc ^ kswz<D>(kl + 1)) << 3)) = kreg[2 * j + 1];
+        if (item(i, kl, cc)) {
+          const int off = kl * D + ((cc ^ kswz<D>(kl)) << 3);
+          *reinterpret_cast<half8*>(sK + buf * KBUF + off) = kreg[i];
           // V row-major like K (the PV operands come out of LDS through transposing reads).
-          half_t* vb = sV + buf * VBUF;
-          *reinterpret_cast<half8*>(vb + kl * D + ((cc ^ kswz<D>(kl)) << 3)) = vreg[2 * j];
-          *reinterpret_cast<half8*>(vb + (kl + 1) * D + ((cc ^ kswz<D>(kl + 1)) << 3)) = vreg[2 * j + 1];
+          *reinterpret_cast<half8*>(sV + buf * VBUF + off) = vreg[i];
         }
       }
     };
 
+    // q rows as MFMA B operands, scaled into the exp2 domain (scale * log2 e) on the way in:
+    // exact when the caller already folded the scale into q (cl == 1), one more fp16
+    // rounding of q otherwise.
     half8 qb[MK];
 #pragma unroll
     for (int m = 0; m < MK; ++m) {
       if (row_ok && (DR == D || 16 * m + 8 * hh < DR)) {
         qb[m] = load_half8(a.q + static_cast<int64_t>(t0 + row) * a.q_stride + static_cast<int64_t>(head) * DR +
                            16 * m + 8 * hh);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qb[m][e] = static_cast<half_t>(static_cast<float>(qb[m][e]) * cl);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) qb[m][e] = 0;
@@ -208,7 +231,15 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
     for (int i = 0; i < DT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
-    float m_run = -INFINITY, l_part = 0.0f;
+    // Row state (lane = row, shared by lanes c and c + 32): ref, the exp2-domain offset of
+    // the row's O and sum (-inf until the row has seen a finite score); l_part, this lane's
+    // share of the sum. The S^T accumulators start at -ref (negref; 0 while ref is -inf), so
+    // the MFMAs deliver s - ref and P = exp2(S^T) needs no per-score arithmetic.
+    float ref = -INFINITY, l_part = 0.0f;
+    float16v negref;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negref[r] = 0.0f;
+    bool have_ref = false;  // wave-uniform: every row of the wave has a finite ref
 
     // This wave's 32 kSub keys of the tile in LDS buffer `buf` starting at key k0.
     // MASK: the keys cross a row of this strip (only the diagonal tiles); a separate
@@ -218,57 +249,82 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
       constexpr bool MASK = decltype(mask_tag)::value;
       float16v s[kSub];
 #pragma unroll
-      for (int j = 0; j < kSub; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[j][r] = 0.0f;
-#pragma unroll
       for (int m = 0; m < MK; ++m)
 #pragma unroll
         for (int j = 0; j < kSub; ++j) {
           const half_t* kt = sK + buf * KBUF + (32 * kSub * half + 32 * j + c) * D;
           const half8 ka = *reinterpret_cast<const half8*>(kt + (((2 * m + hh) ^ kswz<D>(c)) << 3));
-          s[j] = mfma32x32x16(ka, qb[m], s[j]);
+          s[j] = mfma32x32x16(ka, qb[m], m == 0 ? negref : s[j]);
         }
-      float mx = -INFINITY;
-      const int lim = qpos - kb - 4 * hh;  // key offsets above this are masked
+      if (MASK) {
+        const int lim = qpos - kb - 4 * hh;  // key offsets above this are masked
 #pragma unroll
-      for (int j = 0; j < kSub; ++j)
+        for (int j = 0; j < kSub; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if (MASK && 32 * j + 8 * (r >> 2) + (r & 3) > lim) s[j][r] = -INFINITY;
-          mx = fmaxf(mx, s[j][r]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // Lazy rescaling: a row keeps its reference maximum until a score exceeds it by more
-      // than 2^8 in the exp2 domain (P <= 256 stays exact to fp16's 11 bits, sums fit in
-      // fp32), so O^T is rescaled on a handful of tiles instead of most of them.
-      const float m_new = (mx - m_run) * cl > 8.0f ? mx : m_run;  // m_run = -inf: takes mx
-      const float base = m_new == -INFINITY ? 0.0f : m_new * cl;
-      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(__builtin_fmaf(m_run, cl, -base));
-      half8 pb[2 * kSub];
-#pragma unroll
-      for (int j = 0; j < kSub; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          pb[2 * j + (r >> 3)][r & 7] = static_cast<half_t>(fast_exp2(__builtin_fmaf(s[j][r], cl, -base)));
-      // Row sum of the fp16 P values (the ones the PV product uses), fp32 accumulation.
-      float psum = 0.0f;
-#pragma unroll
-      for (int u = 0; u < 2 * kSub; ++u)
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const half2_t p2 = {pb[u][e], pb[u][e + 1]};
-          psum = __builtin_amdgcn_fdot2(p2, half2_t{1.0f16, 1.0f16}, psum, false);
-        }
-      l_part = l_part * alpha + psum;
-      // Rescale O^T only if some row's running maximum changed.
-      if (__ballot(m_new != m_run) != 0) {
-#pragma unroll
-        for (int i = 0; i < DT; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+          for (int r = 0; r < 16; ++r)
+            if (32 * j + 8 * (r >> 2) + (r & 3) > lim) s[j][r] = -INFINITY;
       }
-      m_run = m_new;
+      half8 pb[2 * kSub];
+      float psum = 0.0f;
+      // Row sum of the fp16 P values (the ones the PV product uses), fp32 accumulation.
+      auto exp_and_sum = [&](float shift) {
+        psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kSub; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            pb[2 * j + (r >> 3)][r & 7] = static_cast<half_t>(fast_exp2(s[j][r] - shift));
+#pragma unroll
+        for (int u = 0; u < 2 * kSub; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const half2_t p2 = {pb[u][e], pb[u][e + 1]};
+            psum = __builtin_amdgcn_fdot2(p2, half2_t{1.0f16, 1.0f16}, psum, false);
+          }
+      };
+      // Fast path: P = exp2(s - ref) as it stands, accepted while every lane's sum is at
+      // most 2^15 (so no P overflows fp16; NaN and inf fail the test). The reference offset
+      // only moves when a row's scores rise well above it, on a few tiles per row.
+      bool slow = !have_ref;
+      if (!slow) {
+        exp_and_sum(0.0f);
+        slow = __ballot(!(psum <= 32768.0f)) != 0;
+      }
+      if (slow) {
+        // The row maximum (both lanes of the row), a new offset where it exceeds the old one
+        // by more than 2^8, or where the row had none.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kSub; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, s[j][r]);
+        mx = xlane_max(mx);
+        float shift = 0.0f, alpha = 1.0f;
+        if (ref == -INFINITY) {
+          if (mx != -INFINITY) {
+            shift = mx;
+            ref = mx;
+            alpha = 0.0f;
+          }
+        } else if (mx > 8.0f) {
+          shift = mx;
+          ref += mx;
+          alpha = fast_exp2(-mx);
+        }
+        exp_and_sum(shift);
+        l_part *= alpha;
+        if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+          for (int i = 0; i < DT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+        }
+        const float nr = ref == -INFINITY ? 0.0f : -ref;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) negref[r] = nr;
+        have_ref = __ballot(ref == -INFINITY) == 0;
+      }
+      l_part += psum;
       // V^T operand of lane (d, hh) for pb[u]: slots e < 4 hold keys kr .. kr + 3 and slots
       // e >= 4 keys kr + 8 .. kr + 11 (the S^T accumulator order), kr = 32 (u / 2) + 16 (u % 2)
       // + 4 hh; each run of 4 keys is one transposing read in which lane i16 of the 16-lane
@@ -329,18 +385,18 @@ __global__ __launch_bounds__(kThreads) void flash_prefill_kernel(const PrefillAr
       for (int i = 0; i < DT; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) xo[(i * 16 + r) * 64 + lane] = o[i][r];
-      xml[lane] = m_run;
+      xml[lane] = ref;
       xml[64 + lane] = l_part;
     }
     __syncthreads();
     if (!half && row_ok) {
-      // The even wave saw key 0, so its maximum is finite; the odd one's may not be.
+      // The even wave saw key 0, so its offset is finite; the odd one's may not be.
       const float m_b = xml[lane], l_b = xml[64 + lane];
-      const float m = fmaxf(m_run, m_b);
-      const float fa = fast_exp2((m_run - m) * cl);
-      const float fb = m_b == -INFINITY ? 0.0f : fast_exp2((m_b - m) * cl);
+      const float m = fmaxf(ref, m_b);
+      const float fa = fast_exp2(ref - m);
+      const float fb = m_b == -INFINITY ? 0.0f : fast_exp2(m_b - m);
       const float l = l_part * fa + l_b * fb;
-      const float inv = 1.0f / (l + __shfl_xor(l, 32));
+      const float inv = 1.0f / (l + xlane_sum(l));
       half_t* orow = a.out + static_cast<int64_t>(t0 + row) * a.out_stride + static_cast<int64_t>(head) * DR;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)

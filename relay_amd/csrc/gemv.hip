@@ -91,6 +91,7 @@ struct RopeArgs {
   half_t* kc;
   half_t* vc;
   half_t* q_out;  // [T, heads * D] or null
+  float q_scale;  // q_out = fp16(fp32(q * q_scale))
   int heads, kv_heads, D, block_size;
 };
 
@@ -147,7 +148,7 @@ __device__ __forceinline__ void rope_epilogue(const RopeArgs& ra, const float (&
     }
     qkv[static_cast<int64_t>(t) * N + h * D + j] = out;
     if (h < ra.heads) {
-      if (ra.q_out) ra.q_out[static_cast<int64_t>(t) * ra.heads * D + h * D + j] = static_cast<half_t>(out);
+      if (ra.q_out) ra.q_out[static_cast<int64_t>(t) * ra.heads * D + h * D + j] = f16_of_product(out, ra.q_scale);
     } else if (h < ra.heads + ra.kv_heads) {
       ra.kc[kv_base + j] = static_cast<half_t>(out);
     } else {
@@ -746,11 +747,12 @@ extern "C" int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scal
 extern "C" int rh_gemv_int8_qkv(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
                                 float* qkv, int T, int K, const float* bias, const float* inv_freq, const int* pos,
                                 const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
-                                void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+                                void* q_out, float q_scale, int heads, int kv_heads, int head_dim, int block_size,
+                                void* stream) {
   if (int rc = check_rope(inv_freq, pos, seq, table_off, tables, kpool, vpool, heads, kv_heads, head_dim, block_size))
     return rc;
   RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
-              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+              static_cast<half_t*>(q_out), q_scale, heads, kv_heads, head_dim, block_size};
   const int N = (heads + 2 * kv_heads) * head_dim;
   return int8_fused<kPlain, kRope>(w8, ldw, scale, scale_is_f16, x, nullptr, 0.0f, qkv, T, K, N, 0.0f, stream, ra);
 }
@@ -759,14 +761,14 @@ extern "C" int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const voi
                                         const float* x, const float* norm_w, float eps, float* qkv, int T, int K,
                                         const float* bias, const float* inv_freq, const int* pos, const int* seq,
                                         const int* table_off, const int* tables, void* kpool, void* vpool,
-                                        void* q_out, int heads, int kv_heads, int head_dim, int block_size,
-                                        void* stream) {
+                                        void* q_out, float q_scale, int heads, int kv_heads, int head_dim,
+                                        int block_size, void* stream) {
   RH_REQUIRE(norm_w != nullptr && reinterpret_cast<uintptr_t>(norm_w) % 16 == 0,
              "gemv_int8_rmsnorm_qkv: norm weights missing or not 16-byte aligned");
   if (int rc = check_rope(inv_freq, pos, seq, table_off, tables, kpool, vpool, heads, kv_heads, head_dim, block_size))
     return rc;
   RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
-              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+              static_cast<half_t*>(q_out), q_scale, heads, kv_heads, head_dim, block_size};
   const int N = (heads + 2 * kv_heads) * head_dim;
   return int8_fused<kRmsNorm, kRope>(w8, ldw, scale, scale_is_f16, x, norm_w, eps, qkv, T, K, N, 0.0f, stream, ra);
 }
@@ -869,13 +871,13 @@ extern "C" int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, f
 extern "C" int rh_gemv_f16_qkv(const void* w16, int64_t ldw, const void* x, float* qkv, int T, int K,
                                const float* bias, const float* inv_freq, const int* pos, const int* seq,
                                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out,
-                               int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+                               float q_scale, int heads, int kv_heads, int head_dim, int block_size, void* stream) {
   RH_REQUIRE(inv_freq && pos && seq && table_off && tables && kpool && vpool, "gemv_f16_qkv: missing pointer");
   RH_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gemv_f16_qkv: bad head counts");
   RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "gemv_f16_qkv: head_dim must be a multiple of 16");
   RH_REQUIRE(block_size > 0, "gemv_f16_qkv: bad block size");
   RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
-              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+              static_cast<half_t*>(q_out), q_scale, heads, kv_heads, head_dim, block_size};
   const int N = (heads + 2 * kv_heads) * head_dim;
   return gemv_f16_launch<kPlain, kRope>(w16, ldw, x, nullptr, 0.0f, qkv, T, K, N, 0.0f, stream, ra);
 }
@@ -883,8 +885,8 @@ extern "C" int rh_gemv_f16_qkv(const void* w16, int64_t ldw, const void* x, floa
 extern "C" int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps,
                                        float* qkv, int T, int K, const float* bias, const float* inv_freq,
                                        const int* pos, const int* seq, const int* table_off, const int* tables,
-                                       void* kpool, void* vpool, void* q_out, int heads, int kv_heads, int head_dim,
-                                       int block_size, void* stream) {
+                                       void* kpool, void* vpool, void* q_out, float q_scale, int heads, int kv_heads,
+                                       int head_dim, int block_size, void* stream) {
   RH_REQUIRE(norm_w != nullptr && inv_freq && pos && seq && table_off && tables && kpool && vpool,
              "gemv_f16_rmsnorm_qkv: missing pointer");
   RH_REQUIRE(reinterpret_cast<uintptr_t>(norm_w) % 16 == 0, "gemv_f16_rmsnorm_qkv: norm weights not 16-byte aligned");
@@ -892,7 +894,7 @@ extern "C" int rh_gemv_f16_rmsnorm_qkv(const void* w16, int64_t ldw, const float
   RH_REQUIRE(head_dim > 0 && head_dim % 16 == 0, "gemv_f16_rmsnorm_qkv: head_dim must be a multiple of 16");
   RH_REQUIRE(block_size > 0, "gemv_f16_rmsnorm_qkv: bad block size");
   RopeArgs ra{bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
-              static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size};
+              static_cast<half_t*>(q_out), q_scale, heads, kv_heads, head_dim, block_size};
   const int N = (heads + 2 * kv_heads) * head_dim;
   return gemv_f16_launch<kRmsNorm, kRope>(w16, ldw, x, norm_w, eps, qkv, T, K, N, 0.0f, stream, ra);
 }

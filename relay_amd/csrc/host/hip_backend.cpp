@@ -560,6 +560,10 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
   }
 
   const float eps = static_cast<float>(c_.rms_eps), scale = 1.0f / std::sqrt(static_cast<float>(D));
+  // The fast attention kernels take q already in their exp2 domain: the q writers round
+  // q * scale * log2(e) to fp16 once, and the kernels get scale = ln 2, i.e. a unit
+  // multiplier (scale * log2(e) rounds to exactly 1.0f).
+  const float q_scale = scale * 1.4426950408889634f, attn_scale = 0.6931471805599453f;
   HIP_CHECK(hipEventRecord(fwd_begin_, stream_));
   RH_CHECK(rh_embed(d_tok, T, embed_.p, H, x_.p, stream_));
   for (int l = 0; l < c_.layers; ++l) {
@@ -573,17 +577,17 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       if (L.wqkv.i8.p)
         RH_CHECK(rh_gemv_int8_rmsnorm_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, x_.p, L.attn_norm.p, eps, qkv_.p,
                                           T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out,
-                                          c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+                                          q_scale, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
       else
         RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
-                                         d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
-                                         layout_.block_size, stream_));
+                                         d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads,
+                                         D, layout_.block_size, stream_));
     } else if (L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 && T <= 16 && (QKV + 15) / 16 <= 256) {
       // int8: the projection and qkv_post in one launch (its 16-row tiles in one round;
       // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms).
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_int8_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, xn_.p, qkv_.p, T, H, bias, inv_freq_.p,
-                                d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads, c_.kv_heads, D,
+                                d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D,
                                 layout_.block_size, stream_));
     } else if (!L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 &&
                (T <= 16 || (T <= rh_gemv_f16_max_tokens() && QKV <= 4096)) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
@@ -592,27 +596,27 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       // The projection and qkv_post in one launch (the RMSNorm cannot be folded in here).
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_f16_qkv(L.wqkv.f16.p, H, xn_.p, qkv_.p, T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab,
-                               kc, vc, q_out, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+                               kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     } else {
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
       // The fast kernels read only the fp16 q and the cache; the reference kernel reads qkv.
       if (q_out)
         RH_CHECK(rh_qkv_post_to_cache(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out,
-                                      c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
+                                      q_scale, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
       else
-        RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, c_.heads,
-                             c_.kv_heads, D, layout_.block_size, stream_));
+        RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, 1.0f,
+                             c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     }
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
     if (observer) observer->kv_written(l);
     if (fast_attention_) {
       if (n_work)
         RH_CHECK(rh_flash_prefill(qh_.p, Q, kc, vc, d_tab, d_work, n_work, c_.heads, c_.kv_heads, D,
-                                  layout_.block_size, scale, attn_.p, Q, stream_));
+                                  layout_.block_size, attn_scale, attn_.p, Q, stream_));
       if (n_dec)
         RH_CHECK(rh_paged_decode_attention(qh_.p, Q, kc, vc, d_dec, d_tab, n_dec, c_.heads,
-                                           c_.kv_heads, D, layout_.block_size, slice, parts, scale,
+                                           c_.kv_heads, D, layout_.block_size, slice, parts, attn_scale,
                                            part_o_.p, part_ml_.p, counters_.p, attn_.p, Q, stream_));
     } else {
       RH_CHECK(rh_reference_attention(qkv_.p, QKV, kc, vc, d_pos, d_seq, d_toff, d_tab, nullptr, T, c_.heads,

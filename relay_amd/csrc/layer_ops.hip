@@ -141,7 +141,7 @@ __global__ void rmsnorm_vec_kernel(const float* x, const int* rows, const float*
 template <bool WRITE_BACK>
 __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_freq, const int* pos, const int* seq,
                                 const int* table_off, const int* tables, half_t* kc, half_t* vc, half_t* q_out,
-                                int heads, int kv_heads, int D, int block_size) {
+                                float q_scale, int heads, int kv_heads, int D, int block_size) {
   const int t = blockIdx.x, half = D / 2;
   const int idx = blockIdx.y * kThreads + threadIdx.x;
   if (idx >= (heads + 2 * kv_heads) * half) return;
@@ -170,8 +170,8 @@ __global__ void qkv_post_kernel(float* qkv, const float* bias, const float* inv_
   }
   if (h < heads) {
     if (q_out) {
-      q_out[static_cast<int64_t>(t) * Q + h * D + i] = static_cast<half_t>(a);
-      q_out[static_cast<int64_t>(t) * Q + h * D + i + half] = static_cast<half_t>(b);
+      q_out[static_cast<int64_t>(t) * Q + h * D + i] = f16_of_product(a, q_scale);
+      q_out[static_cast<int64_t>(t) * Q + h * D + i + half] = f16_of_product(b, q_scale);
     }
     return;
   }
@@ -400,8 +400,8 @@ int rh_rmsnorm(const float* x, const int* rows, int R, const float* w, int H, fl
 }
 
 int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, const int* pos, const int* seq,
-                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, int heads,
-                int kv_heads, int head_dim, int block_size, void* stream) {
+                const int* table_off, const int* tables, void* kpool, void* vpool, void* q_out, float q_scale,
+                int heads, int kv_heads, int head_dim, int block_size, void* stream) {
   if (T == 0) return 0;
   RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
              "qkv_post: bad shape");
@@ -409,14 +409,15 @@ int rh_qkv_post(float* qkv, int T, const float* bias, const float* inv_freq, con
   RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel<true>, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads), 0,
                                    static_cast<hipStream_t>(stream), qkv,
                                    bias, inv_freq, pos, seq, table_off, tables, static_cast<half_t*>(kpool),
-                                   static_cast<half_t*>(vpool), static_cast<half_t*>(q_out), heads, kv_heads,
+                                   static_cast<half_t*>(vpool), static_cast<half_t*>(q_out), q_scale, heads, kv_heads,
                                    head_dim, block_size));
   return 0;
 }
 
 int rh_qkv_post_to_cache(const float* qkv, int T, const float* bias, const float* inv_freq, const int* pos,
                          const int* seq, const int* table_off, const int* tables, void* kpool, void* vpool,
-                         void* q_out, int heads, int kv_heads, int head_dim, int block_size, void* stream) {
+                         void* q_out, float q_scale, int heads, int kv_heads, int head_dim, int block_size,
+                         void* stream) {
   if (T == 0) return 0;
   RH_REQUIRE(T > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && block_size > 0,
              "qkv_post_to_cache: bad shape");
@@ -425,7 +426,7 @@ int rh_qkv_post_to_cache(const float* qkv, int T, const float* bias, const float
   RH_TRY_LAUNCH(hipLaunchKernelGGL(qkv_post_kernel<false>, dim3(T, (pairs + kThreads - 1) / kThreads), dim3(kThreads),
                                    0, static_cast<hipStream_t>(stream), const_cast<float*>(qkv), bias, inv_freq, pos,
                                    seq, table_off, tables, static_cast<half_t*>(kpool), static_cast<half_t*>(vpool),
-                                   static_cast<half_t*>(q_out), heads, kv_heads, head_dim, block_size));
+                                   static_cast<half_t*>(q_out), q_scale, heads, kv_heads, head_dim, block_size));
   return 0;
 }
 

@@ -8,6 +8,10 @@ The exact value is computed in float64 from the same fp16 values (numpy as the c
 import numpy as np
 import pytest
 
+# q_out scale passed to the fused q writers and to rh_qkv_post alike (the backend passes the
+# softmax scale times log2(e); any value must give the same bytes on both paths)
+QS = 0.125 * 1.4426950408889634
+
 pytestmark = pytest.mark.gpu
 
 EPS32 = 2.0 ** -24
@@ -231,17 +235,17 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
         if fused and not norm:
             _lib.check(L.rh_gemv_f16_qkv(W.data_ptr(), H, xn.data_ptr(), qkv.data_ptr(), T, H, bp, inv.data_ptr(),
                                          P.data_ptr(), S.data_ptr(), TO.data_ptr(), TB.data_ptr(), kc.data_ptr(),
-                                         vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs, None), "rh_gemv_f16_qkv")
+                                         vc.data_ptr(), qo.data_ptr(), QS, heads, kvh, D, bs, None), "rh_gemv_f16_qkv")
         elif fused:
             _lib.check(L.rh_gemv_f16_rmsnorm_qkv(W.data_ptr(), H, x.data_ptr(), nw.data_ptr(), 1e-5, qkv.data_ptr(), T, H,
                                                  bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
-                                                 TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh,
-                                                 D, bs, None), "rh_gemv_f16_rmsnorm_qkv")
+                                                 TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), QS, heads,
+                                                 kvh, D, bs, None), "rh_gemv_f16_rmsnorm_qkv")
         else:
             _lib.check(L.rh_gemv_f16(W.data_ptr(), H, xn.data_ptr(), qkv.data_ptr(), T, H, N, 0.0, None), "rh_gemv_f16")
             _lib.check(L.rh_qkv_post(qkv.data_ptr(), T, bp, inv.data_ptr(), P.data_ptr(), S.data_ptr(), TO.data_ptr(),
-                                     TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs,
-                                     None), "rh_qkv_post")
+                                     TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), QS, heads, kvh, D,
+                                     bs, None), "rh_qkv_post")
         torch.cuda.synchronize()
         return [a.cpu().numpy() for a in (qkv, kc, vc, qo)]
 

@@ -11,6 +11,10 @@ import pytest
 import oracle as O
 from helpers import bits_to_f32, f16_bits
 
+# q_out scale passed to the fused q writers and to rh_qkv_post alike (the backend passes the
+# softmax scale times log2(e); any value must give the same bytes on both paths)
+QS = 0.125 * 1.4426950408889634
+
 pytestmark = pytest.mark.gpu
 
 EPS32 = 2.0 ** -24
@@ -244,7 +248,7 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
         xn = torch.empty((T, H), dtype=torch.int16, device=dev)
         _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
         rope = (bp, inv.data_ptr(), P.data_ptr(), Sq.data_ptr(), TO.data_ptr(), TB.data_ptr(), kc.data_ptr(),
-                vc.data_ptr(), qo.data_ptr(), heads, kvh, D, bs, None)
+                vc.data_ptr(), qo.data_ptr(), QS, heads, kvh, D, bs, None)
         if fused and not norm:
             _lib.check(L.rh_gemv_int8_qkv(W.data_ptr(), ldw, S.data_ptr(), 0, xn.data_ptr(), qkv.data_ptr(), T, H, *rope),
                        "rh_gemv_int8_qkv")

@@ -149,8 +149,8 @@ def test_qkv_post_places_kv_bit_exact(torch_mod, dev, bs):
     vc = torch_mod.zeros_like(kc)
     qo = torch_mod.empty(T * Q, dtype=torch_mod.int16, device=dev)
     _lib.check(_lib.lib().rh_qkv_post(QKVt.data_ptr(), T, B.data_ptr(), inv0.data_ptr(), P.data_ptr(), S.data_ptr(),
-                                      TO.data_ptr(), TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), heads,
-                                      kvh, D, bs, None))
+                                      TO.data_ptr(), TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), 1.0,
+                                      heads, kvh, D, bs, None))
     torch_mod.cuda.synchronize()
     row = qkv + bias  # fp32 adds, as the kernel does
     k_cache = kc.cpu().numpy().view(np.uint16)
@@ -193,7 +193,7 @@ def test_qkv_post_rope_matches_oracle(torch_mod, dev):
     TOFF, TABS = dt(np.array(toff, np.int32)), dt(np.array(tables, np.int32))
     _lib.check(_lib.lib().rh_qkv_post(X.data_ptr(), T, None, INV.data_ptr(), POS.data_ptr(), SEQ.data_ptr(),
                                       TOFF.data_ptr(), TABS.data_ptr(), kc.data_ptr(), vc.data_ptr(), None,
-                                      heads, kvh, D, bs, None))
+                                      1.0, heads, kvh, D, bs, None))
     torch_mod.cuda.synchronize()
     got = X.cpu().numpy()
     half = D // 2
@@ -280,6 +280,7 @@ def test_qkv_post_to_cache_matches_qkv_post(torch_mod, dev, bs):
     P, S, TO, TB = dt(np.array(pos, np.int32)), dt(np.array(seq, np.int32)), dt(np.array([0, nb0], np.int32)), \
         dt(np.array(tables, np.int32))
     outs = []
+    q_scale = 0.125 * 1.4426950408889634  # softmax scale * log2(e) at head size 64, as the backend passes
     for fn in ("rh_qkv_post", "rh_qkv_post_to_cache"):
         X = dt(qkv)
         kc = torch_mod.full((nblocks * kvh * bs * D,), 0x7BFF, dtype=torch_mod.int16, device=dev)
@@ -288,12 +289,15 @@ def test_qkv_post_to_cache_matches_qkv_post(torch_mod, dev, bs):
         print(f"{fn}: T={T} bs={bs}", flush=True)
         _lib.check(getattr(_lib.lib(), fn)(X.data_ptr(), T, B.data_ptr(), INV.data_ptr(), P.data_ptr(), S.data_ptr(),
                                            TO.data_ptr(), TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(),
-                                           heads, kvh, D, bs, None), fn)
+                                           q_scale, heads, kvh, D, bs, None), fn)
         torch_mod.cuda.synchronize()
         outs.append([a.cpu().numpy() for a in (X, kc, vc, qo)])
     (x0, k0, v0, q0), (x1, k1, v1, q1) = outs
     assert np.array_equal(k0, k1) and np.array_equal(v0, v1) and np.array_equal(q0, q1)
     assert np.array_equal(x1, qkv) and not np.array_equal(x0, qkv)
-    assert _lib.lib().rh_qkv_post_to_cache(None, 1, None, None, None, None, None, None, None, None, None, 8, 2, 64, 16,
-                                           None) != 0
+    # q_out = fp16(rotated q * q_scale), the product rounded once
+    want_q = (x0[:, :Q] * np.float32(q_scale)).astype(np.float16)
+    assert np.array_equal(q0.view(np.float16).reshape(T, Q), want_q)
+    assert _lib.lib().rh_qkv_post_to_cache(None, 1, None, None, None, None, None, None, None, None, None, 1.0, 8, 2, 64,
+                                           16, None) != 0
     assert "q_out is required" in _lib.last_error()
