@@ -32,7 +32,9 @@ class LtGemm {
   // so y is written once whatever beta is.
   bool run(const void* W, const void* x, float* y, int T, int K, int N, float beta);
 
-  static constexpr int kCandidates = 16;
+  // 64 rather than 16 heuristic candidates: TinyLlama's 32 x 2048 decode step 1.70 -> 1.66 ms
+  // (its 32-token products), the 2048-token prefill and the Llama-3 mixed step level.
+  static constexpr int kCandidates = 64;
   static constexpr std::size_t kWorkspaceBytes = std::size_t(128) << 20;
   // Written before each timed candidate call: more than the 256 MB Infinity Cache.
   static constexpr std::size_t kFlushBytes = std::size_t(320) << 20;
