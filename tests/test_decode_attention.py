@@ -8,21 +8,30 @@ the softmax weights and its output to fp16, so |gpu - oracle| <= 2e-3 * max|orac
 Bit-exact: the same logical cache under any block-table permutation, any block size,
 or inside any batch gives identical output bits.
 """
+import copy
 import math
 
 import numpy as np
 import pytest
 
 import oracle as O
-from helpers import PagedCase, bits_to_f32
+from helpers import PagedCase, bits_to_f32, f16_bits
 
 pytestmark = pytest.mark.gpu
 
 
-def run_decode(torch, dev, case, slice_keys=None, tokens=None, counters=None):
-    """slice_keys None: the planner's choice (rh_decode_slice_keys)."""
+LN2 = 0.6931471805599453  # scale * log2(e) rounds to exactly 1.0f: q taken as already scaled
+
+
+def run_decode(torch, dev, case, slice_keys=None, tokens=None, counters=None, exp2_q=False):
+    """slice_keys None: the planner's choice (rh_decode_slice_keys). exp2_q: q in the backend's
+    form, fp16(fp32(q * scale * log2(e))), with scale = ln 2."""
     from relay_amd import _lib
 
+    if exp2_q:
+        case = copy.copy(case)
+        cl = np.float32(np.float32(1.0 / math.sqrt(case.D)) * np.float32(1.4426950408889634))
+        case.q = f16_bits(bits_to_f32(case.q) * cl)
     d = case.to_device(torch, dev)
     toks = list(range(case.T)) if tokens is None else tokens
     n = len(toks)
@@ -40,7 +49,8 @@ def run_decode(torch, dev, case, slice_keys=None, tokens=None, counters=None):
     print(f"decode case: T={case.T} H={H} KVH={KVH} D={D} bs={case.bs} slice={slice_keys}", flush=True)
     rc = _lib.lib().rh_paged_decode_attention(
         d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), dec.data_ptr(), d["tables"].data_ptr(), n,
-        H, KVH, D, case.bs, slice_keys, max_parts, 1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(),
+        H, KVH, D, case.bs, slice_keys, max_parts, LN2 if exp2_q else 1.0 / math.sqrt(D), part_o.data_ptr(),
+        part_ml.data_ptr(),
         counters.data_ptr(), out.data_ptr(), H * D, None)
     _lib.check(rc, "rh_paged_decode_attention")
     torch.cuda.synchronize()
@@ -65,6 +75,15 @@ def check_close(g, o, tol=2e-3):
 def test_matches_oracle_heads(torch_mod, dev, D, heads, kv_heads):
     case = PagedCase([1, 37, 512, 513, 1500], 1, heads, kv_heads, D, 16, seed=heads + D)
     g, _ = run_decode(torch_mod, dev, case)
+    check_close(g, oracle_out(case))
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+def test_exp2_domain_q_matches_oracle(torch_mod, dev, D):
+    """The backend's call: q already scaled by softmax scale * log2(e) and scale = ln 2 (a
+    unit multiplier inside the kernel), against the oracle on the unscaled q."""
+    case = PagedCase([1, 200, 513, 2048, 3001], 1, 32, 8, D, 16, seed=D + 7)
+    g, _ = run_decode(torch_mod, dev, case, exp2_q=True)
     check_close(g, oracle_out(case))
 
 

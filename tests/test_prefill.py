@@ -5,6 +5,7 @@ Each case is a batch of chunks: chunk s holds the last n_new[s] positions of a
 sequence of context ctx[s] (a chunk at an offset sees the earlier chunks' keys through
 the paged cache, as with relay's chunked prefill). Oracle and tolerance as for decode.
 """
+import copy
 import math
 
 import numpy as np
@@ -27,17 +28,30 @@ def chunks_of(case):
     return chunks
 
 
-def run_prefill(torch, dev, case):
+LN2 = 0.6931471805599453  # scale * log2(e) rounds to exactly 1.0f: q taken as already scaled
+
+
+def exp2_domain_q(case):
+    """The backend's form of q: fp16(fp32(q * scale * log2(e))), as its q writers store it."""
+    cl = np.float32(np.float32(1.0 / math.sqrt(case.D)) * np.float32(1.4426950408889634))
+    return f16_bits(bits_to_f32(case.q) * cl)
+
+
+def run_prefill(torch, dev, case, exp2_q=False):
     from relay_amd import _lib
 
     L = _lib.lib()
+    if exp2_q:
+        case = copy.copy(case)
+        case.q = exp2_domain_q(case)
     d = case.to_device(torch, dev)
     H, KVH, D = case.heads, case.kv_heads, case.D
     work = torch.from_numpy(_lib.prefill_work(chunks_of(case), H)).to(dev)
     out = torch.full((case.T, H * D), float("nan"), dtype=torch.float16, device=dev)
     print(f"prefill case: T={case.T} work={work.shape[0]} H={H} KVH={KVH} D={D} bs={case.bs}", flush=True)
     rc = L.rh_flash_prefill(d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(), d["tables"].data_ptr(),
-                            work.data_ptr(), work.shape[0], H, KVH, D, case.bs, 1.0 / math.sqrt(D), out.data_ptr(),
+                            work.data_ptr(), work.shape[0], H, KVH, D, case.bs, LN2 if exp2_q else 1.0 / math.sqrt(D),
+                            out.data_ptr(),
                             H * D, None)
     _lib.check(rc, "rh_flash_prefill")
     torch.cuda.synchronize()
@@ -95,6 +109,14 @@ def test_config3_shape(torch_mod, dev):
     """BASELINE config 3's prefill: one 2048-token prompt, 32 q / 4 kv heads, D 64."""
     case = PagedCase([2048], [2048], 32, 4, 64, 16, seed=0)
     check_close(run_prefill(torch_mod, dev, case), oracle_out(case))
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+def test_exp2_domain_q_matches_oracle(torch_mod, dev, D):
+    """The backend's call: q already scaled by softmax scale * log2(e) and scale = ln 2 (a
+    unit multiplier inside the kernel), against the oracle on the unscaled q."""
+    case = PagedCase([700, 300, 129], [700, 200, 129], 32, 4, D, 16, seed=D + 5)
+    check_close(run_prefill(torch_mod, dev, case, exp2_q=True), oracle_out(case))
 
 
 @pytest.mark.parametrize("D", [64, 128])
