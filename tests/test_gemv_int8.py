@@ -20,6 +20,12 @@ pytestmark = pytest.mark.gpu
 EPS32 = 2.0 ** -24
 
 
+def vector_alu(T, N):
+    """Whether rh_gemv_int8 takes its vector-ALU kernel (one token, or two up to 4096 rows)
+    instead of the MFMA tile for this shape."""
+    return T == 1 or (T == 2 and (N + 7) // 8 <= 512)
+
+
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
     """ldw None: relay's dense rows; otherwise rows ldw bytes apart with junk in the padding."""
     from relay_amd import _lib
@@ -118,15 +124,17 @@ def test_llama3_shapes(torch_mod, dev, N, K, T):
 @pytest.mark.parametrize("N,K", [(2560, 2048), (11264, 2048), (32000, 2048), (2048, 5632), (28672, 4096),
                                  (9, 16), (17, 4112)])
 @pytest.mark.parametrize("f16_scale", [False, True])
-def test_one_token_kernel(torch_mod, dev, N, K, f16_scale):
+@pytest.mark.parametrize("T", [1, 2])
+def test_one_token_kernel(torch_mod, dev, N, K, f16_scale, T):
     """T = 1 on each launch shape of the vector-ALU kernel (16 waves up to 512 workgroups, else
     8, or 4 at K <= 2048; TinyLlama's and Llama-3's projections and LM heads, a K that ends
-    mid-step, a last workgroup with one row), with beta = 1 over a finite y."""
+    mid-step, a last workgroup with one row), T = 2 (its two-token form up to 4096 rows, the
+    MFMA tile above), with beta = 1 over a finite y."""
     from relay_amd import _lib
 
-    w8, s, x = make(N, K, 1, seed=N * 7 + K)
+    w8, s, x = make(N, K, T, seed=N * 7 + K + T)
     s_used = bits_to_f32(f16_bits(s)) if f16_scale else s
-    y0 = np.random.default_rng(N).standard_normal((1, N)).astype(np.float32)
+    y0 = np.random.default_rng(N).standard_normal((T, N)).astype(np.float32)
     y = run(torch_mod, dev, w8, s, x, beta=1.0, y0=y0, f16_scale=f16_scale, ldw=_lib.lib().rh_gemv_int8_row_stride(K))
     exact = O.gemv_int8(w8, s_used, x, beta=1.0, y0=y0)
     assert (np.abs(y - exact) <= bound(w8, s_used, x) + 2 * EPS32 * np.abs(exact)).all()
@@ -156,8 +164,8 @@ def test_rejects_bad_shapes(torch_mod, dev):
 # Fused producers and the qkv epilogue on the int8 GEMV: the same bits as the launches they
 # replace (rh_rmsnorm / rh_silu_mul, rh_gemv_int8, rh_qkv_post), whose parts are checked
 # against their own references (test_layer_ops.py and the tests above), wherever the two use
-# the same kernel and wave split of K (above one token, every shape with at most 256 16-row
-# tiles, the backend's use); against the float64 oracle elsewhere.
+# the same kernel and wave split of K (the MFMA tile: above two tokens, or two above 4096 rows;
+# every shape with at most 256 16-row tiles, the backend's use); against the float64 oracle elsewhere.
 def _fused_vs_chain(torch, dev, kind, T, K, N, beta, f16_scale, seed):
     from relay_amd import _lib
 
@@ -201,10 +209,10 @@ def _fused_vs_chain(torch, dev, kind, T, K, N, beta, f16_scale, seed):
                                                   (4, 2048, 4104, 0.0, True)])
 def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta, f16_scale):
     want, got, (w8, s, xb, y0) = _fused_vs_chain(torch_mod, dev, kind, T, K, N, beta, f16_scale, seed=T + K + N)
-    if T > 1:
+    if not vector_alu(T, N):
         assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
     else:
-        # one token: the plain launch runs the vector-ALU kernel, the fused one the MFMA tile
+        # the plain launch runs the vector-ALU kernel, the fused one the MFMA tile
         exact = O.gemv_int8(w8, s, xb, beta=beta, y0=y0)
         tol = bound(w8, s, xb) + 2 * EPS32 * np.abs(exact)
         assert (np.abs(got - exact) <= tol).all() and (np.abs(want - exact) <= tol).all()
@@ -237,7 +245,7 @@ def test_fused_limits(torch_mod, dev):
 def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias, norm):
     """rh_gemv_int8_rmsnorm_qkv (norm) or rh_gemv_int8_qkv (x already normalised) against
     rh_rmsnorm -> rh_gemv_int8 -> rh_qkv_post. Without rotation (inv_freq = 0) every byte of
-    qkv, q and both caches is equal (above one token; at T = 1 the bounds below). With RoPE the inlined sincosf/products of the two kernels
+    qkv, q and both caches is equal (where rh_gemv_int8 takes the MFMA tile; else the bounds below). With RoPE the inlined sincosf/products of the two kernels
     round differently in the last bit, so rotated fp32 values must agree within 4 ulp of the
     pair's magnitude and fp16 values within 1 ulp."""
     from relay_amd import _lib
@@ -290,12 +298,13 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
     assert (N + 15) // 16 <= 256 and (not norm or L.rh_gemv_f16_fused_fits(T, H))
     inv0 = dt(np.zeros(D // 2, np.float32))
     chain0, fused0 = run_qkv(False, inv0), run_qkv(True, inv0)
-    # At one token the chain's plain product runs on the vector-ALU kernel and the fused qkv
-    # product on the MFMA tile: their sums differ in order, each within the fp32-accumulation
-    # bound of the same fp16 operands (gemv bound below, carried through the rotation).
+    # At one token (two up to 4096 rows) the chain's plain product runs on the vector-ALU
+    # kernel and the fused qkv product on the MFMA tile: their sums differ in order, each within
+    # the fp32-accumulation bound of the same fp16 operands (gemv bound below, carried through
+    # the rotation).
     pairs = lambda v: np.broadcast_to(np.abs(v.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True),
                                       (T, N // D, 2, D // 2)).reshape(T, N)
-    if T == 1:
+    if vector_alu(T, N):
         gb = 2 * bound(w8[:, :H], S.cpu().numpy(), chain0[4].view(np.uint16))
         assert (np.abs(chain0[0] - fused0[0]) <= gb + 2 * EPS32 * np.abs(chain0[0])).all()
         for name, a, b in zip(("k cache", "v cache", "q"), chain0[1:4], fused0[1:4]):
@@ -307,7 +316,7 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
     inv = dt((1.0 / 10000.0 ** (np.arange(0, D, 2) / D)).astype(np.float32))
     (qa, ka, va, oa, _), (qb, kb, vb, ob, _) = run_qkv(False, inv), run_qkv(True, inv)
-    bound_q = 4 * 2.0 ** -24 * pairs(qa) + (2 * pairs(gb) if T == 1 else 0.0)
+    bound_q = 4 * 2.0 ** -24 * pairs(qa) + (2 * pairs(gb) if vector_alu(T, N) else 0.0)
     assert (np.abs(qa - qb) <= bound_q).all()
     for name, a, b in (("k cache", ka, kb), ("v cache", va, vb), ("q", oa, ob)):
         diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
