@@ -793,8 +793,7 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
   // Fused launches keep the MFMA tile at one or two tokens too (a vector-ALU form behind the
-  // producers was taken out: a process that ran it inside the backend's decode step ended
-  // with a GPU memory fault whose cause is not found).
+  // producers made TinyLlama int8 decode steps slower).
   const int tiles = (N + 15) / 16;
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(16 * kWave),
@@ -899,6 +898,7 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
              "gemv_int8: ldw must be >= K, < 2^21 and a multiple of 16");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_int8: W8 and x must be 16-byte aligned");
+  RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr && y != nullptr, "gemv_int8: missing pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
   return scale_is_f16 ? launch<true>(w8, ldw, scale, xh, y, T, K, N, beta, s)
@@ -916,6 +916,7 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_f16: W16 and x must be 16-byte aligned");
+  RH_REQUIRE(w16 != nullptr && x != nullptr && y != nullptr, "gemv_f16: missing pointer");
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_f16: T * (K + 8) fp16 activations exceed the fused path's LDS");
   hipStream_t s = static_cast<hipStream_t>(stream);

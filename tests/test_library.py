@@ -62,6 +62,11 @@ def test_kernel_launchers_validate_shapes_before_launching():
     assert lib.rh_flash_prefill(None, 64, None, None, None, None, 1, 4, 3, 64, 16, 0.1, None, 64, None) != 0
     assert lib.rh_prefill_tile_rows() == 128
     assert lib.rh_gemv_int8_max_tokens() == 64
+    # a null weight pointer (an int8-only matrix passed to the fp16 product) is an error, not a launch
+    assert lib.rh_gemv_f16_rmsnorm(None, 576, 16, 32, 1e-5, 48, 1, 576, 3072, 0.0, None) != 0
+    assert "missing pointer" in _lib.last_error()
+    assert lib.rh_gemv_int8(None, 576, 16, 0, 32, 48, 1, 576, 960, 0.0, None) != 0
+    assert "missing pointer" in _lib.last_error()
 
 
 def test_config_parsing_of_the_fixtures():
