@@ -907,6 +907,79 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
 
 extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
 
+namespace relay_hip {
+namespace {
+
+// fp16 weights at one token on the vector ALU, the layout of gemv_int8_t1_kernel: lane (rg =
+// lane / 8, kl = lane % 8) reads the 8 halves W16[r0 + rg, k + 8 kl .. +8), so 8 lanes read
+// 128 contiguous bytes of a row per load instruction, 8 rows per workgroup; v_dot2_f32_f16
+// accumulates in fp32, lane shuffles sum a row's k-lanes and LDS the WAVES waves (which split
+// K in runs of 64) in a fixed order.
+template <int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_f16_t1_kernel(const half_t* __restrict__ wt, int64_t ldw,
+                                                                    const half_t* __restrict__ x, float* y, int K,
+                                                                    int N, float beta) {
+  __shared__ float red[WAVES][8];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int rg = lane >> 3, kl = lane & 7;
+  const int r0 = blockIdx.x * 8;
+  const int nsteps = (K + 63) / 64;
+  const int per = (nsteps + WAVES - 1) / WAVES;
+  const int s0 = w * per, s1 = min(nsteps, s0 + per);
+  const bool writer = threadIdx.x < 8 && r0 + static_cast<int>(threadIdx.x) < N;
+  const float yold = writer && beta != 0.0f ? y[r0 + threadIdx.x] : 0.0f;  // before the weight stream
+  const half_t* wr = wt + static_cast<int64_t>(min(r0 + rg, N - 1)) * ldw + 8 * kl;
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  float acc = 0.0f;
+  for (int st = s0; st < s1; st += DEPTH) {
+    half8 a[DEPTH], xa[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int k = (st + d) * 64 + 8 * kl;
+      const bool live = st + d < s1 && k < K;
+      a[d] = live ? *reinterpret_cast<const half8*>(wr + (st + d) * 64) : zero;
+      xa[d] = live ? *reinterpret_cast<const half8*>(x + k) : zero;
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        acc = __builtin_amdgcn_fdot2(half2_t{a[d][e], a[d][e + 1]}, half2_t{xa[d][e], xa[d][e + 1]}, acc, false);
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (kl == 0) red[w][rg] = acc;
+  __syncthreads();
+  if (writer) {
+    float v = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][threadIdx.x];
+    y[r0 + threadIdx.x] = v + (beta != 0.0f ? beta * yold : 0.0f);
+  }
+}
+
+// Whether a plain one-token product takes gemv_f16_t1_kernel: from 2 Mi weights (4 MB) up,
+// where it measured faster than the MFMA tile (us: TinyLlama 2048 x 2048 5.7 -> 4.2, 2048 ->
+// 11264 13.9 -> 9.0, 2048 -> 32000 27.3 -> 21.6, SmolLM2's 576 -> 49152 head 17.7 -> 10.4,
+// 4096 x 4096 8.8 -> 7.4, 4096 -> 14336 23.7 -> 20.9); below, both take ~4 us of latency.
+// 8 waves of 4 steps, 4 waves where K <= 1024.
+bool f16_t1_takes(int T, int K, int N) { return T == 1 && static_cast<int64_t>(N) * K >= (int64_t{1} << 21); }
+
+int launch_f16_t1(const half_t* wt, int64_t ldw, const half_t* x, float* y, int K, int N, float beta, hipStream_t s) {
+  const int groups = (N + 7) / 8;
+  if (K <= 1024)
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_t1_kernel<4, 4>), dim3(groups), dim3(4 * kWave), 0, s, wt, ldw, x, y, K,
+                                     N, beta));
+  else
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_t1_kernel<8, 4>), dim3(groups), dim3(8 * kWave), 0, s, wt, ldw, x, y, K,
+                                     N, beta));
+  return 0;
+}
+
+}  // namespace
+}  // namespace relay_hip
+
 template <int PRO, int EPI = kStore>
 static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const float* norm_w, float eps, float* y,
                            int T, int K, int N, float beta, void* stream, const RopeArgs& ra = RopeArgs{},
@@ -916,9 +989,9 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16: ldw must be >= K and a multiple of 8");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemv_f16: W16 and x must be 16-byte aligned");
-  RH_REQUIRE(w16 != nullptr && x != nullptr && y != nullptr, "gemv_f16: missing pointer");
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_f16: T * (K + 8) fp16 activations exceed the fused path's LDS");
+  RH_REQUIRE(w16 != nullptr && x != nullptr && y != nullptr, "gemv_f16: missing pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* wt = static_cast<const half_t*>(w16);
   const int tiles = (N + 15) / 16;
@@ -928,6 +1001,8 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_kernel<W, NBLK, PRO, EPI>), dim3(tiles, ksplit), dim3(W * kWave),     \
                                    PRO == kPlain ? 0 : std::max<size_t>(staged, W * NBLK * kWave * 4 * sizeof(float)), s, wt, \
                                    ldw, x, norm_w, eps, y, T, K, N, beta, ra, sp))
+  if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_t1_takes(T, K, N))
+    return launch_f16_t1(wt, ldw, static_cast<const half_t*>(x), y, K, N, beta, s);
   if (T <= kMaxTokens) {
     if (wide) {
       RH_GEMV_F16(16, 1);

@@ -62,6 +62,17 @@ def test_beta_accumulates(torch_mod, dev):
     check(run(torch_mod, dev, w, x, beta=1.0, y0=y0), w, x, beta=1.0, y0=y0)
 
 
+@pytest.mark.parametrize("N,K,ldw", [(49152, 576, 576), (11264, 2048, 2048 + 8), (3641, 1040, 1040), (2048, 1024, 1032),
+                                     (513, 4096, 4096)])
+def test_one_token_kernel(torch_mod, dev, N, K, ldw):
+    """One token from 2 Mi weights up takes the vector-ALU kernel (4 waves at K <= 1024, else 8;
+    SmolLM2's and TinyLlama's heads and gate_up, a row count not a multiple of 8, padded rows),
+    with beta = 1 over a finite y."""
+    w, x = make(N, K, 1, seed=N + K)
+    y0 = np.random.default_rng(K).standard_normal((1, N)).astype(np.float32)
+    check(run(torch_mod, dev, w, x, beta=1.0, y0=y0, ldw=ldw), w, x, beta=1.0, y0=y0)
+
+
 def test_row_stride_gives_the_same_bits(torch_mod, dev):
     w, x = make(200, 96, 9, seed=3)
     a = run(torch_mod, dev, w, x)
