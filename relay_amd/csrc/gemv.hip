@@ -9,8 +9,9 @@
 // of W is the A operand of v_mfma_f32_16x16x32_f16 and the tokens' activations are the
 // B operand (columns = tokens), so the vector ALU only converts weights, once for all
 // tokens, and the kernel stays bound by the weight stream from HBM at every T.
-// At T = 1 (and T = 2 up to 4096 rows) a vector-ALU kernel (gemv_int8_t1_kernel) reads
-// whole lines per row instead and is faster on every measured shape.
+// At T = 1 a vector-ALU kernel (gemv_int8_t1_kernel) and at T = 2-8 an MFMA kernel with
+// another row/k layout (gemv_int8_m8_kernel) read whole lines per row instead, faster on
+// the measured shapes.
 //
 // int8 -> fp16 is exact and branch-free: for a byte b, the fp16 with bits
 // 0x6400 | (b ^ 0x80) is 1024 + b + 128, so subtracting 1152 leaves b (all values are
@@ -618,15 +619,16 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
 }
 
-// One or two tokens: the products on the vector ALU, no MFMA. At T <= 2 the MFMA tile above
-// spends 14-15 of its 16 B columns on zeros and its 16-row loads touch 16 lines per
+// One token: the products on the vector ALU, no MFMA. At T = 1 the MFMA tile above
+// spends 15 of its 16 B columns on zeros and its 16-row loads touch 16 lines per
 // instruction; here lane (row group rg = lane / 8, k-lane kl = lane % 8) reads the 16 bytes
 // W8[r0 + rg, k + 16 kl .. +16), so 8 lanes read one row's 128 contiguous bytes and one load
 // instruction covers 8 whole lines, 8 rows per workgroup. Each lane converts its bytes with
 // int8x8_to_half8 once and accumulates v_dot2_f32_f16 (pairs of exact int8 * fp16 products)
 // in fp32 for each of the NT tokens; the 8 k-lanes of a row are summed with lane shuffles,
 // then the WAVES waves (which split K in runs of 128) in a fixed order in LDS. DEPTH 128-k
-// steps are loaded before any is used.
+// steps are loaded before any is used. (NT = 1 is launched: the two-token form measured
+// slower than gemv_int8_m8_kernel below.)
 template <int WAVES, int DEPTH, int NT, bool F16_SCALE>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_t1_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                      const void* __restrict__ scale,
@@ -697,25 +699,102 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_t1_kernel(const int8_
   }
 }
 
+// Two to eight tokens on the matrix cores with whole-line row loads: the 16 A rows of
+// v_mfma_f32_16x16x32_f16 are 8 W rows x 2 halves of a 128-k step and its 16 B columns are 8
+// tokens x the same 2 halves. Lane (c, g) loads the 16 bytes W8[r0 + c / 2, k + 64 (c % 2) +
+// 16 g ..+16), so one load instruction covers 8 rows x 128 contiguous bytes (the 16-row tile
+// above covers 16 rows x 64 bytes), and its B operand is token c / 2's activations at the
+// same k (zero past T). Of C only the blocks whose row half equals the column half are sums
+// of matching products: lane (j = 2t + h, g) keeps rows 2g and 2g + 1 of half h for token t,
+// a lane shuffle adds the other half, and LDS sums the WAVES waves (which split K in runs of
+// 128) in a fixed order. DEPTH steps are loaded before any is used.
+template <int WAVES, int DEPTH, bool F16_SCALE>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
+                                                                     const void* __restrict__ scale,
+                                                                     const half_t* __restrict__ x, float* y, int T,
+                                                                     int K, int N, float beta) {
+  __shared__ float red[WAVES][8][8];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int r = c >> 1, h = c & 1;  // A row: W row r0 + r, half h; B column: token r, half h
+  const int r0 = blockIdx.x * 8;
+  const int nsteps = (K + 127) / 128;
+  const int per = (nsteps + WAVES - 1) / WAVES;
+  const int s0 = w * per, s1 = min(nsteps, s0 + per);
+  // Thread 8 t + i writes y[t, r0 + i]; its scale and old y are loaded before the weights.
+  const int wt = threadIdx.x >> 3, wn = r0 + (threadIdx.x & 7);
+  const bool writer = threadIdx.x < 8 * T && wn < N;
+  float sc = 0.0f, yold = 0.0f;
+  if (writer) {
+    sc = F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[wn]) : static_cast<const float*>(scale)[wn];
+    if (beta != 0.0f) yold = y[static_cast<int64_t>(wt) * N + wn];
+  }
+  const int8_t* wr = w8 + static_cast<int64_t>(min(r0 + r, N - 1)) * ldw + 64 * h + 16 * g;
+  const bool tok = r < T;
+  const half_t* xr = x + static_cast<int64_t>(tok ? r : 0) * K + 64 * h + 16 * g;
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int st = s0; st < s1; st += DEPTH) {
+    uint4v wv[DEPTH];
+    half8 xa[DEPTH], xb[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int k = (st + d) * 128 + 64 * h + 16 * g;
+      const bool live = st + d < s1 && k < K;
+      wv[d] = live ? *reinterpret_cast<const uint4v*>(wr + (st + d) * 128) : uint4v{0u, 0u, 0u, 0u};
+      xa[d] = live && tok ? load_half8(xr + (st + d) * 128) : zero;
+      xb[d] = live && tok ? load_half8(xr + (st + d) * 128 + 8) : zero;
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      acc = mfma16x16x32(int8x8_to_half8(wv[d][0], wv[d][1]), xa[d], acc);
+      acc = mfma16x16x32(int8x8_to_half8(wv[d][2], wv[d][3]), xb[d], acc);
+    }
+  }
+  // Lane (column 2t + h, g) holds C rows 4g + q = (W row 2g + q / 2, half q % 2).
+  const float m0 = h ? acc[1] : acc[0], m1 = h ? acc[3] : acc[2];
+  const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
+  if (h == 0 && tok) {
+    red[w][r][2 * g] = v0;
+    red[w][r][2 * g + 1] = v1;
+  }
+  __syncthreads();
+  if (writer) {
+    float v = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][threadIdx.x & 7];
+    y[static_cast<int64_t>(wt) * N + wn] = v * sc + (beta != 0.0f ? beta * yold : 0.0f);
+  }
+}
+
 // Waves per workgroup and load depth, measured on Llama-3-8B and TinyLlama shapes (us,
 // against the MFMA tile's). T = 1: up to 512 workgroups (N <= 4096) 16 waves of 2 steps
 // (4096 x 4096 7.4 -> 5.6, 4096 -> 1024 6.4 -> 3.9, 14336 -> 4096 16.2 -> 13.9, 5632 -> 2048
 // 8.5 -> 5.2); more workgroups than that 8 waves of 4 steps (4096 -> 14336 16.3 -> 13.4,
 // 4096 -> 28672 27.6 -> 23.6), or 4 waves at K <= 2048 (2048 -> 11264 8.5 -> 7.2, 2048 ->
-// 32000 17.5 -> 14.2). T = 2, only up to 512 workgroups, 16 waves of 1 step (4096 x 4096 7.6
-// -> 6.9, 4096 -> 1024 6.4 -> 4.4, 2048 -> 2560 5.7 -> 4.3, 5632 -> 2048 8.6 -> 5.5; at N =
-// 14336 the MFMA tile stays ahead, 16.7 against 17.4, and at T = 4 on every shape).
-bool t1_takes(int T, int N) { return T == 1 || (T == 2 && (N + 7) / 8 <= 512); }
+// 32000 17.5 -> 14.2).
+bool t1_takes(int T) { return T == 1; }
+
+// gemv_int8_m8_kernel, 8 waves of 2 steps, at 2-4 tokens on every shape and at 5-8 on
+// matrices up to 32 Mi weights. Measured (us, 16-row tile -> this): T = 2 4096 x 4096 7.6 ->
+// 5.7, 4096 -> 14336 16.7 -> 13.4, 14336 -> 4096 17.6 -> 13.4, 5632 -> 2048 6.2 -> 5.5 (the
+// vector-ALU kernel's two-token form: 6.9, 17.4, -, 5.5); T = 4 4096 x 4096 7.8 -> 6.2,
+// 4096 -> 1024 6.8 -> 4.5, 4096 -> 14336 16.6 -> 15.6, 2048 -> 11264 9.7 -> 7.4, 5632 ->
+// 2048 8.9 -> 5.6; T = 8 4096 x 4096 8.2 -> 7.8, 2048 -> 11264 10.2 -> 9.5, 5632 -> 2048 9.7
+// -> 6.0, but on the 58.7 MB matrices 18.0 -> 19.9 (each 8-row workgroup reads all T
+// activation rows, twice the weight bytes through L2 at T = 8), where the tile stays.
+bool m8_takes(int T, int K, int N) {
+  return T >= 2 && T <= 8 && (T <= 4 || static_cast<int64_t>(N) * K <= (int64_t{32} << 20));
+}
 
 template <bool F16_SCALE>
-int launch_t1(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
-              float beta, hipStream_t s) {
+int launch_t1(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int K, int N, float beta,
+              hipStream_t s) {
   const int groups = (N + 7) / 8;
 #define RH_T1(W, D, NT)                                                                                             \
   RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_t1_kernel<W, D, NT, F16_SCALE>), dim3(groups), dim3(W * kWave), 0, s, \
                                    w8, ldw, scale, x, y, K, N, beta))
-  if (T == 2) RH_T1(16, 1, 2);
-  else if (groups <= 512) RH_T1(16, 2, 1);
+  if (groups <= 512) RH_T1(16, 2, 1);
   else if (K <= 2048) RH_T1(4, 4, 1);
   else RH_T1(8, 4, 1);
 #undef RH_T1
@@ -746,7 +825,12 @@ int even_rows(int n, int cap) {
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
-  if (t1_takes(T, N)) return launch_t1<F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
+  if (t1_takes(T)) return launch_t1<F16_SCALE>(w8, ldw, scale, x, y, K, N, beta, s);
+  if (m8_takes(T, K, N)) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE>), dim3((N + 7) / 8), dim3(8 * kWave), 0, s,
+                                     w8, ldw, scale, x, y, T, K, N, beta));
+    return 0;
+  }
   // Two row tiles per workgroup (sharing the activation operands, half the activation
   // traffic through L2) only while that still leaves >= 192 workgroups: measured at T = 17-64,
   // N = 6144 gains up to 30% and N = 4096 with 128 workgroups loses as much; at T = 4-16 on
@@ -792,7 +876,7 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
                  float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
-  // Fused launches keep the MFMA tile at one or two tokens too (a vector-ALU form behind the
+  // Fused launches keep the 16-row tile at 1-8 tokens too (a vector-ALU form behind the
   // producers made TinyLlama int8 decode steps slower).
   const int tiles = (N + 15) / 16;
   if (tiles < 256) {
