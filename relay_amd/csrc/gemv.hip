@@ -775,17 +775,16 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
 // 32000 17.5 -> 14.2).
 bool t1_takes(int T) { return T == 1; }
 
-// gemv_int8_m8_kernel, 8 waves of 2 steps, at 2-4 tokens on every shape and at 5-8 on
-// matrices up to 32 Mi weights. Measured (us, 16-row tile -> this): T = 2 4096 x 4096 7.6 ->
+// gemv_int8_m8_kernel, 8 waves of 2 steps, at 2-4 tokens on every shape and at 5-8 where K or
+// N is at most 2048. Measured (us, 16-row tile -> this): T = 2 4096 x 4096 7.6 ->
 // 5.7, 4096 -> 14336 16.7 -> 13.4, 14336 -> 4096 17.6 -> 13.4, 5632 -> 2048 6.2 -> 5.5 (the
 // vector-ALU kernel's two-token form: 6.9, 17.4, -, 5.5); T = 4 4096 x 4096 7.8 -> 6.2,
 // 4096 -> 1024 6.8 -> 4.5, 4096 -> 14336 16.6 -> 15.6, 2048 -> 11264 9.7 -> 7.4, 5632 ->
-// 2048 8.9 -> 5.6; T = 8 4096 x 4096 8.2 -> 7.8, 2048 -> 11264 10.2 -> 9.5, 5632 -> 2048 9.7
-// -> 6.0, but on the 58.7 MB matrices 18.0 -> 19.9 (each 8-row workgroup reads all T
-// activation rows, twice the weight bytes through L2 at T = 8), where the tile stays.
-bool m8_takes(int T, int K, int N) {
-  return T >= 2 && T <= 8 && (T <= 4 || static_cast<int64_t>(N) * K <= (int64_t{32} << 20));
-}
+// 2048 8.9 -> 5.6; T = 8 4096 -> 1024 7.4 -> 4.8, 2048 -> 11264 10.2 -> 9.5, 5632 -> 2048
+// 9.7 -> 6.0, but 4096 x 4096 7.6 -> 7.9 and on the 58.7 MB matrices 18.0 -> 19.9 (each 8-row
+// workgroup reads all T activation rows, twice the weight bytes through L2 at T = 8), where
+// the tile stays.
+bool m8_takes(int T, int K, int N) { return T >= 2 && T <= 8 && (T <= 4 || std::min(K, N) <= 2048); }
 
 template <bool F16_SCALE>
 int launch_t1(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int K, int N, float beta,

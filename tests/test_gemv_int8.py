@@ -22,9 +22,9 @@ EPS32 = 2.0 ** -24
 
 def vector_alu(T, N, K):
     """Whether rh_gemv_int8 takes a whole-line kernel (the vector-ALU one at one token, the
-    8-row MFMA one at 2-4 tokens, and at 5-8 up to 32 Mi weights) instead of the 16-row MFMA
-    tile that the fused launches use."""
-    return T == 1 or (2 <= T <= 8 and (T <= 4 or N * K <= 32 << 20))
+    8-row MFMA one at 2-4 tokens, and at 5-8 where K or N is at most 2048) instead of the
+    16-row MFMA tile that the fused launches use."""
+    return T == 1 or (2 <= T <= 8 and (T <= 4 or min(K, N) <= 2048))
 
 
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
@@ -130,7 +130,7 @@ def test_whole_line_kernels(torch_mod, dev, N, K, f16_scale, T):
     """T = 1 on each launch shape of the vector-ALU kernel (16 waves up to 512 workgroups, else
     8, or 4 at K <= 2048; TinyLlama's and Llama-3's projections and LM heads, a K that ends
     mid-step, a last workgroup with one row), T = 2-8 on the 8-row MFMA kernel (the 16-row
-    tile at 5-8 tokens above 32 Mi weights), with beta = 1 over a finite y."""
+    tile at 5-8 tokens where K and N exceed 2048), with beta = 1 over a finite y."""
     from relay_amd import _lib
 
     w8, s, x = make(N, K, T, seed=N * 7 + K + T)
