@@ -1042,6 +1042,81 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_t1_kernel(const half_t
   }
 }
 
+// fp16 weights at 2-8 tokens on the matrix cores with whole-line row loads (the layout of
+// gemv_int8_m8_kernel): the 16 A rows of v_mfma_f32_16x16x32_f16 are 8 W rows x the two 32-k
+// halves of a 64-k step, its 16 B columns 8 tokens x the same halves. Lane (c, g) loads the 8
+// halves W16[r0 + c / 2, k + 32 (c % 2) + 8 g ..+8) straight into its A operand, so one load
+// instruction covers 8 rows x 128 contiguous bytes, and token c / 2's activations at the same
+// k into its B operand (zero past T). The C blocks whose row half matches the column half
+// hold the sums; a lane shuffle adds the halves and LDS the WAVES waves in a fixed order.
+template <int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_f16_m8_kernel(const half_t* __restrict__ wt, int64_t ldw,
+                                                                    const half_t* __restrict__ x, float* y, int T,
+                                                                    int K, int N, float beta) {
+  __shared__ float red[WAVES][8][8];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int r = c >> 1, h = c & 1;
+  const int r0 = blockIdx.x * 8;
+  const int nsteps = (K + 63) / 64;
+  const int per = (nsteps + WAVES - 1) / WAVES;
+  const int s0 = w * per, s1 = min(nsteps, s0 + per);
+  const int wt_ = threadIdx.x >> 3, wn = r0 + (threadIdx.x & 7);
+  const bool writer = threadIdx.x < 8 * T && wn < N;
+  const float yold = writer && beta != 0.0f ? y[static_cast<int64_t>(wt_) * N + wn] : 0.0f;  // before the weights
+  const half_t* wr = wt + static_cast<int64_t>(min(r0 + r, N - 1)) * ldw + 32 * h + 8 * g;
+  const bool tok = r < T;
+  const half_t* xr = x + static_cast<int64_t>(tok ? r : 0) * K + 32 * h + 8 * g;
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int st = s0; st < s1; st += DEPTH) {
+    half8 a[DEPTH], b[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int k = (st + d) * 64 + 32 * h + 8 * g;
+      const bool live = st + d < s1 && k < K;
+      a[d] = live ? load_half8(wr + (st + d) * 64) : zero;
+      b[d] = live && tok ? load_half8(xr + (st + d) * 64) : zero;
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) acc = mfma16x16x32(a[d], b[d], acc);
+  }
+  // Lane (column 2t + h, g) holds C rows 4g + q = (W row 2g + q / 2, half q % 2).
+  const float m0 = h ? acc[1] : acc[0], m1 = h ? acc[3] : acc[2];
+  const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
+  if (h == 0 && tok) {
+    red[w][r][2 * g] = v0;
+    red[w][r][2 * g + 1] = v1;
+  }
+  __syncthreads();
+  if (writer) {
+    float v = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt_][threadIdx.x & 7];
+    y[static_cast<int64_t>(wt_) * N + wn] = v + (beta != 0.0f ? beta * yold : 0.0f);
+  }
+}
+
+// Plain fp16 products at 2-8 tokens take gemv_f16_m8_kernel: 8 waves of 4 steps, 4 waves of 8
+// below 256 workgroups. Measured (us, 16-row tile -> this, T = 2 / 4 / 8): TinyLlama 2048 x
+// 2048 5.8 / 6.0 / 6.2 -> 3.9 / 4.1 / 3.8, 2048 -> 11264 14.3 / 14.8 / 14.7 -> 9.2 / 9.4 /
+// 10.6, 5632 -> 2048 9.8 / 10.1 / 11.2 -> 6.3 / 6.3 / 6.6; 4096 -> 14336 24.2 / 25.8 / 28.6
+// -> 20.9 / 20.8 / 23.3; SmolLM2 1536 -> 576 4.5 / 4.6 / 4.9 -> 3.9 / 4.1 / 4.0, 576 -> 960
+// level (~4.0, latency).
+bool f16_m8_takes(int T) { return T >= 2 && T <= 8; }
+
+int launch_f16_m8(const half_t* wt, int64_t ldw, const half_t* x, float* y, int T, int K, int N, float beta,
+                  hipStream_t s) {
+  const int groups = (N + 7) / 8;
+  if (groups < 256)
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_m8_kernel<4, 8>), dim3(groups), dim3(4 * kWave), 0, s, wt, ldw, x, y, T,
+                                     K, N, beta));
+  else
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_f16_m8_kernel<8, 4>), dim3(groups), dim3(8 * kWave), 0, s, wt, ldw, x, y, T,
+                                     K, N, beta));
+  return 0;
+}
+
 // Whether a plain one-token product takes gemv_f16_t1_kernel: from 2 Mi weights (4 MB) up,
 // where it measured faster than the MFMA tile (us: TinyLlama 2048 x 2048 5.7 -> 4.2, 2048 ->
 // 11264 13.9 -> 9.0, 2048 -> 32000 27.3 -> 21.6, SmolLM2's 576 -> 49152 head 17.7 -> 10.4,
@@ -1086,6 +1161,8 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
                                    ldw, x, norm_w, eps, y, T, K, N, beta, ra, sp))
   if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_t1_takes(T, K, N))
     return launch_f16_t1(wt, ldw, static_cast<const half_t*>(x), y, K, N, beta, s);
+  if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_m8_takes(T))
+    return launch_f16_m8(wt, ldw, static_cast<const half_t*>(x), y, T, K, N, beta, s);
   if (T <= kMaxTokens) {
     if (wide) {
       RH_GEMV_F16(16, 1);

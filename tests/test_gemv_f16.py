@@ -17,6 +17,19 @@ pytestmark = pytest.mark.gpu
 EPS32 = 2.0 ** -24
 
 
+def whole_line(T, N, K):
+    """Whether rh_gemv_f16 takes a whole-line kernel (the vector-ALU one at one token from 2 Mi
+    weights, the 8-row MFMA one at 2-8 tokens) instead of the 16-row MFMA tile that the fused
+    launches use: then the two sum in different orders."""
+    return (T == 1 and N * K >= 1 << 21) or 2 <= T <= 8
+
+
+def gemv_bound(w_f16, x_f16):
+    """fp32-accumulation bound of x w^T for fp16 operands (rows of x against rows of w)."""
+    wd, xd = w_f16.astype(np.float64), x_f16.astype(np.float64)
+    return 4 * w_f16.shape[1] * EPS32 * (np.abs(xd) @ np.abs(wd).T) + 1e-30
+
+
 def run(torch, dev, w, x, beta=0.0, y0=None, ldw=None):
     from relay_amd import _lib
 
@@ -70,6 +83,16 @@ def test_one_token_kernel(torch_mod, dev, N, K, ldw):
     with beta = 1 over a finite y."""
     w, x = make(N, K, 1, seed=N + K)
     y0 = np.random.default_rng(K).standard_normal((1, N)).astype(np.float32)
+    check(run(torch_mod, dev, w, x, beta=1.0, y0=y0, ldw=ldw), w, x, beta=1.0, y0=y0)
+
+
+@pytest.mark.parametrize("N,K,T,ldw", [(11264, 2048, 8, 2048), (576, 1536, 3, 1544), (2048, 5632, 2, 5632),
+                                       (13, 4112, 7, 4120)])
+def test_few_token_kernel(torch_mod, dev, N, K, T, ldw):
+    """2-8 tokens on the 8-row whole-line MFMA kernel (8 waves; 4 below 256 workgroups), padded
+    rows, a K that ends mid-step, a last workgroup with five rows, beta = 1 over a finite y."""
+    w, x = make(N, K, T, seed=N + K + T)
+    y0 = np.random.default_rng(K).standard_normal((T, N)).astype(np.float32)
     check(run(torch_mod, dev, w, x, beta=1.0, y0=y0, ldw=ldw), w, x, beta=1.0, y0=y0)
 
 
@@ -153,13 +176,15 @@ def test_rejects_bad_shapes(torch_mod, dev):
 
 # Fused producers: rh_gemv_f16_rmsnorm / rh_gemv_f16_silu must give the same bits as the
 # two-launch chain they replace (rh_rmsnorm or rh_silu_mul, then rh_gemv_f16), whose parts
-# are checked against their own references (test_layer_ops.py and the tests above).
+# are checked against their own references (test_layer_ops.py and the tests above), where
+# both take the 16-row tile; within the fp32 bound where the plain launch takes another kernel.
 def _chain_and_fused(torch, dev, kind, T, K, N, beta, seed):
     from relay_amd import _lib
 
     L = _lib.lib()
     rng = np.random.default_rng(seed)
-    W = torch.from_numpy((rng.standard_normal((N, K)) * 0.05).astype(np.float16).view(np.int16)).to(dev)
+    w16 = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    W = torch.from_numpy(w16.view(np.int16)).to(dev)
     y0 = rng.standard_normal((T, N)).astype(np.float32)
     want = torch.from_numpy(y0.copy()).to(dev)
     got = torch.from_numpy(y0.copy()).to(dev)
@@ -178,7 +203,7 @@ def _chain_and_fused(torch, dev, kind, T, K, N, beta, seed):
                    "rh_gemv_f16_silu")
     _lib.check(L.rh_gemv_f16(W.data_ptr(), K, xh.data_ptr(), want.data_ptr(), T, K, N, beta, None), "rh_gemv_f16")
     torch.cuda.synchronize()
-    return want.cpu().numpy(), got.cpu().numpy()
+    return want.cpu().numpy(), got.cpu().numpy(), w16, xh.cpu().numpy().view(np.float16)
 
 
 @pytest.mark.parametrize("kind", ["rmsnorm", "silu"])
@@ -190,8 +215,11 @@ def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta):
     from relay_amd import _lib
 
     assert _lib.lib().rh_gemv_f16_fused_fits(T, K)
-    want, got = _chain_and_fused(torch_mod, dev, kind, T, K, N, beta, seed=T + K + N)
-    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
+    want, got, w16, xh = _chain_and_fused(torch_mod, dev, kind, T, K, N, beta, seed=T + K + N)
+    if whole_line(T, N, K):  # the chain's plain launch sums in another order
+        assert (np.abs(want - got) <= 2 * gemv_bound(w16, xh) + 4 * EPS32 * np.abs(want)).all()
+    else:
+        assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
 
 
 def test_fused_limits(torch_mod, dev):
@@ -211,8 +239,8 @@ def test_fused_limits(torch_mod, dev):
 def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias, norm):
     """rh_gemv_f16_rmsnorm_qkv (norm) or rh_gemv_f16_qkv (x already normalised) against
     rh_rmsnorm -> rh_gemv_f16 -> rh_qkv_post.
-    Without rotation (inv_freq = 0) every byte of qkv, q and both caches is equal: same sums,
-    same placement. With RoPE the two kernels' inlined sincosf/products round differently in
+    Without rotation (inv_freq = 0) every byte of qkv, q and both caches is equal where the
+    plain launch takes the 16-row tile too (same sums, same placement); else the bounds below. With RoPE the two kernels' inlined sincosf/products round differently in
     the last bit (measured: ~20% of rotated values 1 ulp apart), so rotated fp32 values must
     agree within 4 ulp of the pair's magnitude and fp16 values within 1 ulp."""
     from relay_amd import _lib
@@ -228,7 +256,8 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
     nblocks = 2 * per + 3
     tables = [int(b) for b in rng.permutation(nblocks)[:2 * per]]
     dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    W = dt((rng.standard_normal((N, H)) * 0.05).astype(np.float16).view(np.int16))
+    w16 = (rng.standard_normal((N, H)) * 0.05).astype(np.float16)
+    W = dt(w16.view(np.int16))
     x = dt((rng.standard_normal((T, H)) * 2).astype(np.float32))
     nw = dt(rng.uniform(0.5, 1.5, H).astype(np.float32))
     bias = dt(rng.standard_normal(N).astype(np.float32)) if with_bias else None
@@ -258,18 +287,40 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
                                      TB.data_ptr(), kc.data_ptr(), vc.data_ptr(), qo.data_ptr(), QS, heads, kvh, D,
                                      bs, None), "rh_qkv_post")
         torch.cuda.synchronize()
-        return [a.cpu().numpy() for a in (qkv, kc, vc, qo)]
+        return [a.cpu().numpy() for a in (qkv, kc, vc, qo, xn)]
 
     print(f"fused qkv: T={T} heads={heads}/{kvh} D={D} H={H} bs={bs} bias={with_bias} norm={norm}", flush=True)
     inv0 = dt(np.zeros(D // 2, np.float32))
-    for name, a, b in zip(("qkv", "k cache", "v cache", "q"), run(False, inv0), run(True, inv0)):
-        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+    chain0, fused0 = run(False, inv0), run(True, inv0)
+    # Where the chain's plain launch takes a whole-line kernel the two sum in different orders:
+    # fp32 values within twice the accumulation bound, fp16 ones within that plus one rounding.
+    loose = whole_line(T, N, H)
+    gb = 2 * gemv_bound(w16, chain0[4].view(np.float16)) if loose else np.zeros((T, N))
+    if loose:
+        assert (np.abs(chain0[0] - fused0[0]) <= gb + 2 * EPS32 * np.abs(chain0[0])).all()
+        for name, a, b in zip(("k cache", "v cache", "q"), chain0[1:4], fused0[1:4]):
+            f16_close(a, b, gb.max(), name)
+    else:
+        for name, a, b in zip(("qkv", "k cache", "v cache", "q"), chain0[:4], fused0[:4]):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
     inv = dt((1.0 / 10000.0 ** (np.arange(0, D, 2) / D)).astype(np.float32))
-    (qa, ka, va, oa), (qb, kb, vb, ob) = run(False, inv), run(True, inv)
+    (qa, ka, va, oa, _), (qb, kb, vb, ob, _) = run(False, inv), run(True, inv)
     # fp32: the magnitude of a rotated value is bounded by |a| + |b| of its pair
-    pair = np.abs(qa.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True)
-    bound = 4 * 2.0 ** -24 * np.broadcast_to(pair, (T, N // D, 2, D // 2)).reshape(T, N)
+    pairs = lambda v: np.broadcast_to(np.abs(v.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True),
+                                      (T, N // D, 2, D // 2)).reshape(T, N)
+    bound = 4 * 2.0 ** -24 * pairs(qa) + 2 * pairs(gb)
     assert (np.abs(qa - qb) <= bound).all()
     for name, a, b in (("k cache", ka, kb), ("v cache", va, vb), ("q", oa, ob)):
-        diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
-        assert diff.max() <= 1 and (np.sign(a) == np.sign(b)).all(), name
+        if loose:
+            f16_close(a, b, 2 * gb.max(), name)
+        else:
+            diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
+            assert diff.max() <= 1 and (np.sign(a) == np.sign(b)).all(), name
+
+
+def f16_close(a_bits, b_bits, tol, name):
+    """fp16 outputs of two fp32 values at most tol apart: within tol plus one fp16 rounding."""
+    va = a_bits.view(np.float16).astype(np.float64)
+    vb = b_bits.view(np.float16).astype(np.float64)
+    lim = tol + 2.0 ** -10 * np.maximum(np.abs(va), np.abs(vb)) + 2.0 ** -24
+    assert (np.abs(va - vb) <= lim).all(), name
