@@ -9,9 +9,8 @@
 // of W is the A operand of v_mfma_f32_16x16x32_f16 and the tokens' activations are the
 // B operand (columns = tokens), so the vector ALU only converts weights, once for all
 // tokens, and the kernel stays bound by the weight stream from HBM at every T.
-// At T = 1 a vector-ALU kernel (gemv_int8_t1_kernel) and at T = 2-8 an MFMA kernel with
-// another row/k layout (gemv_int8_m8_kernel) read whole lines per row instead, faster on
-// the measured shapes.
+// At T = 1-8 an MFMA kernel with another row/k layout (gemv_int8_m8_kernel) reads whole lines
+// per row instead, faster on the measured shapes.
 //
 // int8 -> fp16 is exact and branch-free: for a byte b, the fp16 with bits
 // 0x6400 | (b ^ 0x80) is 1024 + b + 128, so subtracting 1152 leaves b (all values are
@@ -619,87 +618,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
   }
 }
 
-// One token: the products on the vector ALU, no MFMA. At T = 1 the MFMA tile above
-// spends 15 of its 16 B columns on zeros and its 16-row loads touch 16 lines per
-// instruction; here lane (row group rg = lane / 8, k-lane kl = lane % 8) reads the 16 bytes
-// W8[r0 + rg, k + 16 kl .. +16), so 8 lanes read one row's 128 contiguous bytes and one load
-// instruction covers 8 whole lines, 8 rows per workgroup. Each lane converts its bytes with
-// int8x8_to_half8 once and accumulates v_dot2_f32_f16 (pairs of exact int8 * fp16 products)
-// in fp32 for each of the NT tokens; the 8 k-lanes of a row are summed with lane shuffles,
-// then the WAVES waves (which split K in runs of 128) in a fixed order in LDS. DEPTH 128-k
-// steps are loaded before any is used. (NT = 1 is launched: the two-token form measured
-// slower than gemv_int8_m8_kernel below.)
-template <int WAVES, int DEPTH, int NT, bool F16_SCALE>
-__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_t1_kernel(const int8_t* __restrict__ w8, int64_t ldw,
-                                                                     const void* __restrict__ scale,
-                                                                     const half_t* __restrict__ x, float* y, int K,
-                                                                     int N, float beta) {
-  __shared__ float red[WAVES][NT][8];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int rg = lane >> 3, kl = lane & 7;
-  const int r0 = blockIdx.x * 8;
-  const int nsteps = (K + 127) / 128;
-  const int per = (nsteps + WAVES - 1) / WAVES;
-  const int s0 = w * per, s1 = min(nsteps, s0 + per);
-  // Thread (token t, row r0 + i) = 8 t + i writes y. Its scale and old y are loaded before
-  // the weight stream (issued after the reduction they would queue behind it).
-  const int wt = threadIdx.x >> 3, wn = r0 + (threadIdx.x & 7);
-  const bool writer = threadIdx.x < 8 * NT && wn < N;
-  float sc = 0.0f, yold = 0.0f;
-  if (writer) {
-    sc = F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[wn]) : static_cast<const float*>(scale)[wn];
-    if (beta != 0.0f) yold = y[static_cast<int64_t>(wt) * N + wn];
-  }
-  const int8_t* wr = w8 + static_cast<int64_t>(min(r0 + rg, N - 1)) * ldw + 16 * kl;
-  float acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int st = s0; st < s1; st += DEPTH) {
-    uint4v wv[DEPTH];
-    half8 xa[NT][DEPTH], xb[NT][DEPTH];
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int k = (st + d) * 128 + 16 * kl;
-      const bool live = st + d < s1 && k < K;
-      wv[d] = live ? *reinterpret_cast<const uint4v*>(wr + (st + d) * 128) : uint4v{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        xa[t][d] = live ? *reinterpret_cast<const half8*>(x + t * K + k) : zero;
-        xb[t][d] = live ? *reinterpret_cast<const half8*>(x + t * K + k + 8) : zero;
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const half8 a = int8x8_to_half8(wv[d][0], wv[d][1]);
-      const half8 b = int8x8_to_half8(wv[d][2], wv[d][3]);
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          acc[t] = __builtin_amdgcn_fdot2(half2_t{a[e], a[e + 1]}, half2_t{xa[t][d][e], xa[t][d][e + 1]}, acc[t], false);
-          acc[t] = __builtin_amdgcn_fdot2(half2_t{b[e], b[e + 1]}, half2_t{xb[t][d][e], xb[t][d][e + 1]}, acc[t], false);
-        }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    float v = acc[t];
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    if (kl == 0) red[w][t][rg] = v;
-  }
-  __syncthreads();
-  if (writer) {
-    float v = 0.0f;
-#pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][threadIdx.x & 7];
-    y[static_cast<int64_t>(wt) * N + wn] = v * sc + (beta != 0.0f ? beta * yold : 0.0f);
-  }
-}
-
-// Two to eight tokens on the matrix cores with whole-line row loads: the 16 A rows of
+// One to eight tokens on the matrix cores with whole-line row loads: the 16 A rows of
 // v_mfma_f32_16x16x32_f16 are 8 W rows x 2 halves of a 128-k step and its 16 B columns are 8
 // tokens x the same 2 halves. Lane (c, g) loads the 16 bytes W8[r0 + c / 2, k + 64 (c % 2) +
 // 16 g ..+16), so one load instruction covers 8 rows x 128 contiguous bytes (the 16-row tile
@@ -767,16 +686,10 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
   }
 }
 
-// Waves per workgroup and load depth, measured on Llama-3-8B and TinyLlama shapes (us,
-// against the MFMA tile's). T = 1: up to 512 workgroups (N <= 4096) 16 waves of 2 steps
-// (4096 x 4096 7.4 -> 5.6, 4096 -> 1024 6.4 -> 3.9, 14336 -> 4096 16.2 -> 13.9, 5632 -> 2048
-// 8.5 -> 5.2); more workgroups than that 8 waves of 4 steps (4096 -> 14336 16.3 -> 13.4,
-// 4096 -> 28672 27.6 -> 23.6), or 4 waves at K <= 2048 (2048 -> 11264 8.5 -> 7.2, 2048 ->
-// 32000 17.5 -> 14.2).
-bool t1_takes(int T) { return T == 1; }
-
-// gemv_int8_m8_kernel, 8 waves of 2 steps, at 2-4 tokens on every shape and at 5-8 where K or
-// N is at most 2048. Measured (us, 16-row tile -> this): T = 2 4096 x 4096 7.6 ->
+// gemv_int8_m8_kernel, 8 waves of 2 steps, at 1-4 tokens on every shape and at 5-8 where K or
+// N is at most 2048. Measured (us, 16-row tile -> this): T = 1 4096 x 4096 7.4 -> 5.3, 4096 ->
+// 14336 16.3 -> 13.1, 14336 -> 4096 16.2 -> 13.1, 2048 -> 11264 8.5 -> 6.8 (a vector-ALU
+// kernel with 8 lanes per 128-byte row run and v_dot2_f32_f16 took 5.6-6.4, 14.2, 13.9, 7.7); T = 2 4096 x 4096 7.6 ->
 // 5.7, 4096 -> 14336 16.7 -> 13.4, 14336 -> 4096 17.6 -> 13.4, 5632 -> 2048 6.2 -> 5.5 (the
 // vector-ALU kernel's two-token form: 6.9, 17.4, -, 5.5); T = 4 4096 x 4096 7.8 -> 6.2,
 // 4096 -> 1024 6.8 -> 4.5, 4096 -> 14336 16.6 -> 15.6, 2048 -> 11264 9.7 -> 7.4, 5632 ->
@@ -784,21 +697,7 @@ bool t1_takes(int T) { return T == 1; }
 // 9.7 -> 6.0, but 4096 x 4096 7.6 -> 7.9 and on the 58.7 MB matrices 18.0 -> 19.9 (each 8-row
 // workgroup reads all T activation rows, twice the weight bytes through L2 at T = 8), where
 // the tile stays.
-bool m8_takes(int T, int K, int N) { return T >= 2 && T <= 8 && (T <= 4 || std::min(K, N) <= 2048); }
-
-template <bool F16_SCALE>
-int launch_t1(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int K, int N, float beta,
-              hipStream_t s) {
-  const int groups = (N + 7) / 8;
-#define RH_T1(W, D, NT)                                                                                             \
-  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_t1_kernel<W, D, NT, F16_SCALE>), dim3(groups), dim3(W * kWave), 0, s, \
-                                   w8, ldw, scale, x, y, K, N, beta))
-  if (groups <= 512) RH_T1(16, 2, 1);
-  else if (K <= 2048) RH_T1(4, 4, 1);
-  else RH_T1(8, 4, 1);
-#undef RH_T1
-  return 0;
-}
+bool m8_takes(int T, int K, int N) { return T >= 1 && T <= 8 && (T <= 4 || std::min(K, N) <= 2048); }
 
 template <int NB, int RT, bool F16_SCALE>
 int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
@@ -824,7 +723,6 @@ int even_rows(int n, int cap) {
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
-  if (t1_takes(T)) return launch_t1<F16_SCALE>(w8, ldw, scale, x, y, K, N, beta, s);
   if (m8_takes(T, K, N)) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE>), dim3((N + 7) / 8), dim3(8 * kWave), 0, s,
                                      w8, ldw, scale, x, y, T, K, N, beta));
@@ -875,8 +773,8 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
                  float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
-  // Fused launches keep the 16-row tile at 1-8 tokens too (a vector-ALU form behind the
-  // producers made TinyLlama int8 decode steps slower).
+  // Fused launches keep the 16-row tile at 1-8 tokens too (a one-token vector-ALU form
+  // behind the producers made TinyLlama int8 decode steps slower).
   const int tiles = (N + 15) / 16;
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(16 * kWave),
@@ -993,7 +891,7 @@ extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }
 namespace relay_hip {
 namespace {
 
-// fp16 weights at one token on the vector ALU, the layout of gemv_int8_t1_kernel: lane (rg =
+// fp16 weights at one token on the vector ALU: lane (rg =
 // lane / 8, kl = lane % 8) reads the 8 halves W16[r0 + rg, k + 8 kl .. +8), so 8 lanes read
 // 128 contiguous bytes of a row per load instruction, 8 rows per workgroup; v_dot2_f32_f16
 // accumulates in fp32, lane shuffles sum a row's k-lanes and LDS the WAVES waves (which split

@@ -226,7 +226,9 @@ def test_library_gemm_choices_agree(dev, monkeypatch):
         got[mode] = be.forward(b)
         be.close()
     cpu = O.CpuBackend(w, 16, 16).forward(b)
-    assert rel_err_rowmax(got["default"], got["rocblas"]) < 1e-3
+    # hipBLASLt's kernel is chosen by timing, so the pair's summation orders vary between runs
+    # (measured up to 1.07e-3 apart); each is held to the oracle's 2e-3 below.
+    assert rel_err_rowmax(got["default"], got["rocblas"]) < 2e-3
     assert (got["default"].argmax(axis=1) == got["rocblas"].argmax(axis=1)).mean() >= 0.98
     for mode in got:
         assert rel_err_rowmax(got[mode], cpu) < 2e-3, mode

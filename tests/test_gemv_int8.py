@@ -21,10 +21,9 @@ EPS32 = 2.0 ** -24
 
 
 def vector_alu(T, N, K):
-    """Whether rh_gemv_int8 takes a whole-line kernel (the vector-ALU one at one token, the
-    8-row MFMA one at 2-4 tokens, and at 5-8 where K or N is at most 2048) instead of the
-    16-row MFMA tile that the fused launches use."""
-    return T == 1 or (2 <= T <= 8 and (T <= 4 or min(K, N) <= 2048))
+    """Whether rh_gemv_int8 takes the 8-row whole-line MFMA kernel (1-4 tokens, and 5-8 where K
+    or N is at most 2048) instead of the 16-row MFMA tile that the fused launches use."""
+    return 1 <= T <= 8 and (T <= 4 or min(K, N) <= 2048)
 
 
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
@@ -109,7 +108,7 @@ def test_fp16_scales(torch_mod, dev):
 @pytest.mark.parametrize("T", [1, 8, 48])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
 def test_llama3_shapes(torch_mod, dev, N, K, T):
-    """BASELINE config 4's projection shapes at one token (the vector-ALU kernel), T = 8 and
+    """BASELINE config 4's projection shapes at one token (the 8-row whole-line kernel), T = 8 and
     config 5's 48 decode tokens (fp16 scales), in the padded row layout the backend stores
     (rh_gemv_int8_row_stride)."""
     from relay_amd import _lib
@@ -127,10 +126,9 @@ def test_llama3_shapes(torch_mod, dev, N, K, T):
 @pytest.mark.parametrize("f16_scale", [False, True])
 @pytest.mark.parametrize("T", [1, 2, 3, 5, 8])
 def test_whole_line_kernels(torch_mod, dev, N, K, f16_scale, T):
-    """T = 1 on each launch shape of the vector-ALU kernel (16 waves up to 512 workgroups, else
-    8, or 4 at K <= 2048; TinyLlama's and Llama-3's projections and LM heads, a K that ends
-    mid-step, a last workgroup with one row), T = 2-8 on the 8-row MFMA kernel (the 16-row
-    tile at 5-8 tokens where K and N exceed 2048), with beta = 1 over a finite y."""
+    """T = 1-8 on the 8-row whole-line MFMA kernel (the 16-row tile at 5-8 tokens where K and
+    N exceed 2048): TinyLlama's and Llama-3's projections and LM heads, a K that ends mid-step,
+    a last workgroup with one row, with beta = 1 over a finite y."""
     from relay_amd import _lib
 
     w8, s, x = make(N, K, T, seed=N * 7 + K + T)
@@ -213,7 +211,7 @@ def test_fused_producers_match_the_chain(torch_mod, dev, kind, T, K, N, beta, f1
     if not vector_alu(T, N, K):
         assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
     else:
-        # the plain launch runs the vector-ALU kernel, the fused one the MFMA tile
+        # the plain launch runs the 8-row whole-line kernel, the fused one the 16-row tile
         exact = O.gemv_int8(w8, s, xb, beta=beta, y0=y0)
         tol = bound(w8, s, xb) + 2 * EPS32 * np.abs(exact)
         assert (np.abs(got - exact) <= tol).all() and (np.abs(want - exact) <= tol).all()
@@ -308,8 +306,8 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
     assert (N + 15) // 16 <= 256 and (not norm or L.rh_gemv_f16_fused_fits(T, H))
     inv0 = dt(np.zeros(D // 2, np.float32))
     chain0, fused0 = run_qkv(False, inv0), run_qkv(True, inv0)
-    # At one token (two up to 4096 rows) the chain's plain product runs on the vector-ALU
-    # kernel and the fused qkv product on the MFMA tile: their sums differ in order, each within
+    # Where the chain's plain product runs on the 8-row whole-line kernel and the fused qkv
+    # product on the 16-row tile, their sums differ in order, each within
     # the fp32-accumulation bound of the same fp16 operands (gemv bound below, carried through
     # the rotation).
     pairs = lambda v: np.broadcast_to(np.abs(v.reshape(T, -1, 2, D // 2)).sum(axis=2, keepdims=True),
