@@ -627,61 +627,74 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 // of matching products: lane (j = 2t + h, g) keeps rows 2g and 2g + 1 of half h for token t,
 // a lane shuffle adds the other half, and LDS sums the WAVES waves (which split K in runs of
 // 128) in a fixed order. DEPTH steps are loaded before any is used.
-template <int WAVES, int DEPTH, bool F16_SCALE>
+template <int WAVES, int DEPTH, bool F16_SCALE, int RT = 1>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                      const void* __restrict__ scale,
                                                                      const half_t* __restrict__ x, float* y, int T,
                                                                      int K, int N, float beta) {
-  __shared__ float red[WAVES][8][8];
+  // RT 8-row groups per workgroup share each B operand (activation loads) through L2 once.
+  __shared__ float red[WAVES][8][8 * RT];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int r = c >> 1, h = c & 1;  // A row: W row r0 + r, half h; B column: token r, half h
-  const int r0 = blockIdx.x * 8;
+  const int r = c >> 1, h = c & 1;  // A row: W row r0 + 8 rt + r, half h; B column: token r, half h
+  const int r0 = blockIdx.x * 8 * RT;
   const int nsteps = (K + 127) / 128;
   const int per = (nsteps + WAVES - 1) / WAVES;
   const int s0 = w * per, s1 = min(nsteps, s0 + per);
-  // Thread 8 t + i writes y[t, r0 + i]; its scale and old y are loaded before the weights.
-  const int wt = threadIdx.x >> 3, wn = r0 + (threadIdx.x & 7);
-  const bool writer = threadIdx.x < 8 * T && wn < N;
+  // Thread 8 RT t + i writes y[t, r0 + i]; its scale and old y are loaded before the weights.
+  const int wt = threadIdx.x / (8 * RT), wn = r0 + static_cast<int>(threadIdx.x % (8 * RT));
+  const bool writer = static_cast<int>(threadIdx.x) < 8 * RT * T && wn < N;
   float sc = 0.0f, yold = 0.0f;
   if (writer) {
     sc = F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[wn]) : static_cast<const float*>(scale)[wn];
     if (beta != 0.0f) yold = y[static_cast<int64_t>(wt) * N + wn];
   }
-  const int8_t* wr = w8 + static_cast<int64_t>(min(r0 + r, N - 1)) * ldw + 64 * h + 16 * g;
+  const int8_t* wr[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    wr[rt] = w8 + static_cast<int64_t>(min(r0 + 8 * rt + r, N - 1)) * ldw + 64 * h + 16 * g;
   const bool tok = r < T;
   const half_t* xr = x + static_cast<int64_t>(tok ? r : 0) * K + 64 * h + 16 * g;
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float4v acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   for (int st = s0; st < s1; st += DEPTH) {
-    uint4v wv[DEPTH];
+    uint4v wv[DEPTH][RT];
     half8 xa[DEPTH], xb[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int k = (st + d) * 128 + 64 * h + 16 * g;
       const bool live = st + d < s1 && k < K;
-      wv[d] = live ? *reinterpret_cast<const uint4v*>(wr + (st + d) * 128) : uint4v{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        wv[d][rt] = live ? *reinterpret_cast<const uint4v*>(wr[rt] + (st + d) * 128) : uint4v{0u, 0u, 0u, 0u};
       xa[d] = live && tok ? load_half8(xr + (st + d) * 128) : zero;
       xb[d] = live && tok ? load_half8(xr + (st + d) * 128 + 8) : zero;
     }
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      acc = mfma16x16x32(int8x8_to_half8(wv[d][0], wv[d][1]), xa[d], acc);
-      acc = mfma16x16x32(int8x8_to_half8(wv[d][2], wv[d][3]), xb[d], acc);
-    }
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]), xa[d], acc[rt]);
+        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]), xb[d], acc[rt]);
+      }
   }
   // Lane (column 2t + h, g) holds C rows 4g + q = (W row 2g + q / 2, half q % 2).
-  const float m0 = h ? acc[1] : acc[0], m1 = h ? acc[3] : acc[2];
-  const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
-  if (h == 0 && tok) {
-    red[w][r][2 * g] = v0;
-    red[w][r][2 * g + 1] = v1;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float m0 = h ? acc[rt][1] : acc[rt][0], m1 = h ? acc[rt][3] : acc[rt][2];
+    const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
+    if (h == 0 && tok) {
+      red[w][r][8 * rt + 2 * g] = v0;
+      red[w][r][8 * rt + 2 * g + 1] = v1;
+    }
   }
   __syncthreads();
   if (writer) {
     float v = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][threadIdx.x & 7];
+    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][threadIdx.x % (8 * RT)];
     y[static_cast<int64_t>(wt) * N + wn] = v * sc + (beta != 0.0f ? beta * yold : 0.0f);
   }
 }
@@ -694,9 +707,11 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
 // vector-ALU kernel's two-token form: 6.9, 17.4, -, 5.5); T = 4 4096 x 4096 7.8 -> 6.2,
 // 4096 -> 1024 6.8 -> 4.5, 4096 -> 14336 16.6 -> 15.6, 2048 -> 11264 9.7 -> 7.4, 5632 ->
 // 2048 8.9 -> 5.6; T = 8 4096 -> 1024 7.4 -> 4.8, 2048 -> 11264 10.2 -> 9.5, 5632 -> 2048
-// 9.7 -> 6.0, but 4096 x 4096 7.6 -> 7.9 and on the 58.7 MB matrices 18.0 -> 19.9 (each 8-row
-// workgroup reads all T activation rows, twice the weight bytes through L2 at T = 8), where
-// the tile stays.
+// 9.7 -> 6.0. At 5-8 tokens with K and N above 2048 each 8-row workgroup re-reads all
+// T activation rows (twice the weight bytes through L2 at T = 8: 4096 x 4096 7.6 -> 7.9, the
+// 58.7 MB matrices 18.0 -> 19.9), so those take two 8-row groups per workgroup sharing the
+// activations (RT = 2): T = 8 4096 x 4096 7.5 -> 6.6, 4096 -> 14336 17.7 -> 16.5, 14336 ->
+// 4096 17.7 -> 14.6.
 bool m8_takes(int T, int K, int N) { return T >= 1 && T <= 8 && (T <= 4 || std::min(K, N) <= 2048); }
 
 template <int NB, int RT, bool F16_SCALE>
@@ -726,6 +741,11 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
   if (m8_takes(T, K, N)) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE>), dim3((N + 7) / 8), dim3(8 * kWave), 0, s,
                                      w8, ldw, scale, x, y, T, K, N, beta));
+    return 0;
+  }
+  if (T <= 8) {  // 16 rows per workgroup: half the activation reads of the 8-row form
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 2>), dim3((N + 15) / 16), dim3(8 * kWave), 0,
+                                     s, w8, ldw, scale, x, y, T, K, N, beta));
     return 0;
   }
   // Two row tiles per workgroup (sharing the activation operands, half the activation

@@ -21,9 +21,9 @@ EPS32 = 2.0 ** -24
 
 
 def vector_alu(T, N, K):
-    """Whether rh_gemv_int8 takes the 8-row whole-line MFMA kernel (1-4 tokens, and 5-8 where K
-    or N is at most 2048) instead of the 16-row MFMA tile that the fused launches use."""
-    return 1 <= T <= 8 and (T <= 4 or min(K, N) <= 2048)
+    """Whether rh_gemv_int8 takes the whole-line MFMA kernel (1-8 tokens; 8 or 16 rows per
+    workgroup) instead of the 16-row MFMA tile that the fused launches use."""
+    return 1 <= T <= 8
 
 
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
@@ -126,8 +126,8 @@ def test_llama3_shapes(torch_mod, dev, N, K, T):
 @pytest.mark.parametrize("f16_scale", [False, True])
 @pytest.mark.parametrize("T", [1, 2, 3, 5, 8])
 def test_whole_line_kernels(torch_mod, dev, N, K, f16_scale, T):
-    """T = 1-8 on the 8-row whole-line MFMA kernel (the 16-row tile at 5-8 tokens where K and
-    N exceed 2048): TinyLlama's and Llama-3's projections and LM heads, a K that ends mid-step,
+    """T = 1-8 on the whole-line MFMA kernel (16 rows per workgroup at 5-8 tokens where K and
+    N exceed 2048, else 8): TinyLlama's and Llama-3's projections and LM heads, a K that ends mid-step,
     a last workgroup with one row, with beta = 1 over a finite y."""
     from relay_amd import _lib
 
