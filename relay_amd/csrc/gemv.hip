@@ -699,8 +699,9 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
   }
 }
 
-// gemv_int8_m8_kernel, 8 waves of 2 steps, at 1-4 tokens on every shape and at 5-8 where K or
-// N is at most 2048. Measured (us, 16-row tile -> this): T = 1 4096 x 4096 7.4 -> 5.3, 4096 ->
+// gemv_int8_m8_kernel, 8 waves of 2 steps, 8 rows per workgroup at 1-3 tokens on every shape
+// and at 4-8 where K or N is at most 2048, else 16 (T = 4: 4096 -> 14336 16.0 -> 13.6 us,
+// 14336 -> 4096 15.3 -> 14.2, 4096 x 4096 6.1 -> 6.4). Measured (us, 16-row tile -> this): T = 1 4096 x 4096 7.4 -> 5.3, 4096 ->
 // 14336 16.3 -> 13.1, 14336 -> 4096 16.2 -> 13.1, 2048 -> 11264 8.5 -> 6.8 (a vector-ALU
 // kernel with 8 lanes per 128-byte row run and v_dot2_f32_f16 took 5.6-6.4, 14.2, 13.9, 7.7); T = 2 4096 x 4096 7.6 ->
 // 5.7, 4096 -> 14336 16.7 -> 13.4, 14336 -> 4096 17.6 -> 13.4, 5632 -> 2048 6.2 -> 5.5 (the
@@ -712,7 +713,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
 // 58.7 MB matrices 18.0 -> 19.9), so those take two 8-row groups per workgroup sharing the
 // activations (RT = 2): T = 8 4096 x 4096 7.5 -> 6.6, 4096 -> 14336 17.7 -> 16.5, 14336 ->
 // 4096 17.7 -> 14.6.
-bool m8_takes(int T, int K, int N) { return T >= 1 && T <= 8 && (T <= 4 || std::min(K, N) <= 2048); }
+bool m8_takes(int T, int K, int N) { return T >= 1 && T <= 8 && (T <= 3 || std::min(K, N) <= 2048); }
 
 template <int NB, int RT, bool F16_SCALE>
 int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,

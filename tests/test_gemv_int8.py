@@ -126,7 +126,7 @@ def test_llama3_shapes(torch_mod, dev, N, K, T):
 @pytest.mark.parametrize("f16_scale", [False, True])
 @pytest.mark.parametrize("T", [1, 2, 3, 5, 8])
 def test_whole_line_kernels(torch_mod, dev, N, K, f16_scale, T):
-    """T = 1-8 on the whole-line MFMA kernel (16 rows per workgroup at 5-8 tokens where K and
+    """T = 1-8 on the whole-line MFMA kernel (16 rows per workgroup at 4-8 tokens where K and
     N exceed 2048, else 8): TinyLlama's and Llama-3's projections and LM heads, a K that ends mid-step,
     a last workgroup with one row, with beta = 1 over a finite y."""
     from relay_amd import _lib
