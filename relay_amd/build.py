@@ -76,6 +76,8 @@ def build_oracle() -> None:
         subprocess.run(["make", "-s", "-C", oracle, "-j8", "ref"], check=True)
         # relay's Engine driving the HIP backend (needs the kernel objects of build())
         subprocess.run(["make", "-s", "-C", oracle, "-j8", "engine-hip"], check=True)
+        # relay's own test programs with the RELAY_TEST_BACKEND=hip branch of check.h
+        subprocess.run(["make", "-s", "-C", oracle, "-j8", "ref-tests-hip"], check=True)
 
 
 if __name__ == "__main__":

@@ -563,6 +563,8 @@ __global__ void zero_words_kernel(int* p, int n) {
 
 std::mutex g_noalloc_mu;
 void* g_noalloc_ptr[kMaxDevices] = {};
+hipStream_t g_noalloc_stream[kMaxDevices] = {};  // the stream of the device's last call
+bool g_noalloc_used[kMaxDevices] = {};
 
 // The device address of `scratch` on the current device, looked up (and its counters
 // cleared, by a kernel so that the call may sit inside a captured graph) on the first call
@@ -576,6 +578,22 @@ int noalloc_scratch(hipStream_t s, void** out) {
   }
   RH_REQUIRE(dev >= 0 && dev < kMaxDevices, "decode attention (no-alloc): device index out of range");
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  // Overlap guard: a call on another stream than the device's previous call is refused while
+  // that stream still has work queued (the previous call's kernel may still be using the
+  // array). Calls on one stream are ordered by the stream and need no check. A stream under
+  // graph capture cannot be queried; such calls (and replays of captured graphs) are not
+  // checked.
+  if (g_noalloc_used[dev] && g_noalloc_stream[dev] != s) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone &&
+        hipStreamQuery(g_noalloc_stream[dev]) == hipErrorNotReady) {
+      (void)hipGetLastError();
+      set_error("decode attention (no-alloc): the previous call on this GPU, on another stream, may still be running; "
+                "calls of the no-alloc entry point share one scratch array per GPU and must not overlap");
+      return -1;
+    }
+    (void)hipGetLastError();  // a query of a stream that no longer exists leaves an error behind
+  }
   if (!g_noalloc_ptr[dev]) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -588,6 +606,8 @@ int noalloc_scratch(hipStream_t s, void** out) {
     g_noalloc_ptr[dev] = p;
   }
   *out = g_noalloc_ptr[dev];
+  g_noalloc_stream[dev] = s;
+  g_noalloc_used[dev] = true;
   return 0;
 }
 

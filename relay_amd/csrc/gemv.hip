@@ -787,8 +787,9 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 }
 
 // The int8 product with a fused producer (PRO) and/or the qkv epilogue (EPI): 16-row
-// workgroups, the wave count of the plain launch for the same N (so the sums are the plain
-// product's, bit for bit).
+// workgroups with the wave count of the 16-row tile's plain launch for the same N, so at
+// 9-16 tokens the sums are the plain product's bit for bit; at 1-8 tokens the plain product
+// runs the whole-line kernel (another summation order: equal within the fp32 bound).
 template <bool F16_SCALE, int PRO, int EPI>
 int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* xin, const float* norm_w, float eps,
                  float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {

@@ -30,6 +30,7 @@
 #include <numeric>
 #include <stdexcept>
 #include <string>
+#include <system_error>
 #include <thread>
 
 #include "relay/backend.h"
@@ -688,10 +689,27 @@ void HipBackend::finish_forward(float* dst, std::size_t n) {
       std::memcpy(reinterpret_cast<unsigned char*>(dst) + a, host + a, len);
     }
   };
-  std::vector<std::thread> helpers;
-  for (int j = 1; j < workers; ++j) helpers.emplace_back(copy_share, j);
+  // Helper threads are joined by the guard on every path (a thread that cannot be started
+  // leaves its share to the calling thread), so no exception leaves a joinable thread behind.
+  struct Joiner {
+    std::vector<std::thread> t;
+    ~Joiner() {
+      for (auto& x : t)
+        if (x.joinable()) x.join();
+    }
+  } helpers;
+  int started = 1;
+  for (int j = 1; j < workers; ++j) {
+    try {
+      helpers.t.emplace_back(copy_share, j);
+      ++started;
+    } catch (const std::system_error&) {
+      break;
+    }
+  }
   copy_share(0);
-  for (auto& t : helpers) t.join();
+  for (int j = started; j < workers; ++j) copy_share(j);
+  for (auto& t : helpers.t) t.join();
   if (failed) throw std::runtime_error("HIP error while copying the logits");
 }
 

@@ -105,12 +105,13 @@ def test_fp16_scales(torch_mod, dev):
     assert (np.abs(y - exact) <= bound(w8, s16, x)).all()
 
 
-@pytest.mark.parametrize("T", [1, 8, 48])
+@pytest.mark.parametrize("T", [1, 4, 8, 48])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
 def test_llama3_shapes(torch_mod, dev, N, K, T):
-    """BASELINE config 4's projection shapes at one token (the 8-row whole-line kernel), T = 8 and
-    config 5's 48 decode tokens (fp16 scales), in the padded row layout the backend stores
-    (rh_gemv_int8_row_stride)."""
+    """Llama-3-8B projection shapes at config 4's batch sizes 1, 4 and 8 (the whole-line
+    kernel: 8 rows per workgroup at one token and on 4096 -> 1024; 16 rows at 4 and 8 tokens
+    where K and N exceed 2048) and config 5's 48 decode tokens, fp16 scales, in the padded
+    row layout the backend stores (rh_gemv_int8_row_stride)."""
     from relay_amd import _lib
 
     w8, s, x = make(N, K, T, seed=N + K + T)
@@ -124,7 +125,7 @@ def test_llama3_shapes(torch_mod, dev, N, K, T):
 @pytest.mark.parametrize("N,K", [(2560, 2048), (11264, 2048), (32000, 2048), (2048, 5632), (28672, 4096),
                                  (9, 16), (17, 4112)])
 @pytest.mark.parametrize("f16_scale", [False, True])
-@pytest.mark.parametrize("T", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_whole_line_kernels(torch_mod, dev, N, K, f16_scale, T):
     """T = 1-8 on the whole-line MFMA kernel (16 rows per workgroup at 4-8 tokens where K and
     N exceed 2048, else 8): TinyLlama's and Llama-3's projections and LM heads, a K that ends mid-step,

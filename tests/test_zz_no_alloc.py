@@ -58,3 +58,43 @@ def test_noalloc_rejects_oversize(torch_mod, dev):
     rc = L.rh_paged_decode_attention_noalloc(None, 4096, None, None, None, None, 512, 32, 8, 128, 16, 128, 64,
                                              0.1, None, 4096, None)
     assert rc != 0 and "static scratch" in _lib.last_error()
+
+
+def test_noalloc_refuses_an_overlapping_call_on_another_stream(torch_mod, dev):
+    """While the previous call's stream still has work queued, a call on another stream is
+    refused with an error (both would use the GPU's one scratch array); once that stream has
+    drained, the other stream's call runs and gives the buffered entry point's bits."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    if not hasattr(torch.cuda, "_sleep"):
+        pytest.skip("torch.cuda._sleep is not available")
+    L = _lib.lib()
+    case = PagedCase([700, 1, 513, 1500], 1, 32, 4, 64, 16, seed=23)
+    d = case.to_device(torch, dev)
+    H, KVH, D, n, sk = case.heads, case.kv_heads, case.D, case.T, 256
+    max_parts = max(math.ceil((p + 1) / sk) for p in case.pos)
+    dec = torch.from_numpy(case.dec_meta()).to(dev)
+    out = torch.full((n, H * D), float("nan"), dtype=torch.float16, device=dev)
+
+    def call(stream):
+        return L.rh_paged_decode_attention_noalloc(d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(),
+                                                   dec.data_ptr(), d["tables"].data_ptr(), n, H, KVH, D, case.bs, sk,
+                                                   max_parts, 1 / math.sqrt(D), out.data_ptr(), H * D,
+                                                   stream.cuda_stream)
+
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    print("no-alloc overlap guard: busy stream A, then a call on stream B", flush=True)
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(200_000_000)  # ~0.1 s of queued work on stream A
+    _lib.check(call(sa), "decode attention (no-alloc) on stream A")
+    rc = call(sb)
+    busy = sa.query() is False
+    torch.cuda.synchronize()
+    if busy:
+        assert rc != 0 and "must not overlap" in _lib.last_error()
+    _lib.check(call(sb), "decode attention (no-alloc) on stream B after A drained")
+    torch.cuda.synchronize()
+    want = _call(torch, dev, case, sk, noalloc=False)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
