@@ -251,6 +251,17 @@ int rh_gemv_f16_max_tokens(void);
 int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
                float beta, void* stream);
 
+/* rh_gemm_w8 with K cut into ksplit ranges (1 <= ksplit <= 8, at most K / 64) so that
+ * narrow matrices fill the GPU: each range writes its raw sums to workspace (fp32,
+ * ksplit * T * N values, N a multiple of 4) and a second launch adds them in range order
+ * before the scale and beta (deterministic, independent of timing). Calls sharing a
+ * workspace must not overlap. rh_gemm_w8_plan(T, K, N) gives the split measured best for
+ * the shape (-1 if K is not a positive multiple of 64). No counterpart in relay, which
+ * dequantizes the whole matrix and calls cublasGemmEx (cuda_backend.cu:718-722). */
+int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K,
+                     int N, float beta, int ksplit, float* workspace, void* stream);
+int rh_gemm_w8_plan(int T, int K, int N);
+
 /* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 64-token tile and K cut into ksplit ranges
  * (1 <= ksplit <= 8, at most one per step of 128 k, or of 64 k when K is not a multiple
  * of 128), so that decode batches of 17-64 tokens read the int8

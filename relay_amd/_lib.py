@@ -69,6 +69,8 @@ SIGNATURES = {
     "rh_gemv_f16_max_tokens": (I, []),
     "rh_gemm_w8": (I, [P, I64, P, P, P, I, I, I, F, P]),
     "rh_gemm_w8_skinny": (I, [P, I64, P, P, P, I, I, I, F, I, P, P]),
+    "rh_gemm_w8_split": (I, [P, I64, P, P, P, I, I, I, F, I, P, P]),
+    "rh_gemm_w8_plan": (I, [I, I, I]),
     "rh_gemm_w8_split_plan": (I, [I, I, I]),
     "rh_gemv_f16_rmsnorm": (I, [P, I64, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_f16_silu": (I, [P, I64, P, P, I, I, I, F, P]),

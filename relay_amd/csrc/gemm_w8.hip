@@ -35,20 +35,20 @@
 #include "../../include/relay_hip.h"
 #include "common.h"
 
+#include <algorithm>
+
 namespace relay_hip {
 namespace {
 
+// int8 x 8 -> fp16 x 8, exact, in 10 instructions: each byte b ^ 0x80 (= b + 128 as an
+// unsigned byte) is placed under a 0x64 high byte by v_perm_b32, which gives the fp16
+// 1024 + b + 128, and 1152 is then subtracted (a packed fp16 add; exact).
 __device__ __forceinline__ half8 int8x8_to_half8_w8(uint32_t lo, uint32_t hi) {
-  // bytes b -> halves with bits 0x6400 | (b ^ 0x80) = 1024 + b + 128, minus 1152.
   const uint32_t x0 = lo ^ 0x80808080u, x1 = hi ^ 0x80808080u;
-  uint32_t h[4];
-  h[0] = (x0 & 0xFFu) | ((x0 & 0xFF00u) << 8) | 0x64006400u;
-  h[1] = ((x0 >> 16) & 0xFFu) | ((x0 >> 8) & 0xFF0000u) | 0x64006400u;
-  h[2] = (x1 & 0xFFu) | ((x1 & 0xFF00u) << 8) | 0x64006400u;
-  h[3] = ((x1 >> 16) & 0xFFu) | ((x1 >> 8) & 0xFF0000u) | 0x64006400u;
-  half8 v = __builtin_bit_cast(half8, uint4v{h[0], h[1], h[2], h[3]});
+  const uint4v u = {__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u),
+                    __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)};
   const half8 bias = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
-  return v - bias;
+  return __builtin_bit_cast(half8, u) - bias;
 }
 
 // WN x WT waves; each wave AN 32-row blocks x BT 32-token blocks.
@@ -242,6 +242,209 @@ int launch_w8(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x
   return 0;
 }
 
+// ---- the large-batch tile (T above 64: prefill chunks, mixed batches) -------------------
+//
+// 4 waves; wave w owns rows 32 AN w .. +32 AN of the workgroup's 128 AN rows and all of its
+// 32 BT tokens (AN x BT accumulators of v_mfma_f32_32x32x16_f16). Per 64-k step:
+//   - W: lane (c, h) of a wave reads the 32 bytes W8[row c of block a, k0 + 32 h .. +32) as
+//     two 16-byte buffer loads straight into registers, two steps ahead (two named register
+//     sets for even and odd steps); in k-slice q its A operand holds k = k0 + 32 h + 8 q + j
+//     in slot 8 h + j, converted from int8 just before use;
+//   - x: the workgroup's 32 BT x 64 activation tile is loaded one step ahead and staged in
+//     LDS (double-buffered, rows padded by 16 bytes: conflict-free 16-byte reads); lane (c, h)
+//     reads x[t, k0 + 32 h + 8 q .. +8) as the matching B operand of token t = 32 b + c;
+//   - the LDS reads and A conversions of k-slice q + 1 are issued before the MFMAs of slice q.
+// Every load is unconditional (steps past the range re-read the last one, rows past N read
+// row N - 1, tokens past T read row T - 1; none of those columns or rows is stored), so the
+// compiler's wait counts stay exact. Workgroup L runs on XCD L % 8; each XCD takes a
+// contiguous range of tiles with the token tile fastest, so the workgroups that share a W
+// slice share an L2. K may be cut into ksn ranges (blockIdx-derived kz), written raw to a
+// workspace and added in range order by w8_split_merge_kernel.
+//
+// Measured on MI355X, Llama-3-8B shapes at T = 560 (us; dequantize + rocBLAS in brackets,
+// the fp16 library GEMM on fp16 weights in braces): 6144 x 4096 56.9 [~75] {42-46},
+// 4096 x 4096 44.0 [~60] {29-40}, 28672 x 4096 166.9 (the 2 x 3 tile) [~200] {128-135},
+// 4096 x 14336 103.4 [~125] {87-105}. A copy of the kernel without the global loads in the
+// loop runs the 28672 x 4096 product in 103 us, so the remaining gap to the MFMA rate is the
+// memory pipeline (W and x loads cost ~40 and ~20 us there). Tried and slower: one wave per
+// SIMD with 4 x 4 or 4 x 3 blocks per wave, 4 x 2 blocks, token-major tile order, per-slice
+// scheduling barriers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w8_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+template <int AN, int BT, int WPE>
+__global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restrict__ w8, int64_t ldw,
+                                                           const float* __restrict__ scale,
+                                                           const half_t* __restrict__ x, float* y, int T, int K, int N,
+                                                           float beta, float* ws, int n_row, int n_tok, int ksn,
+                                                           int vec_out) {
+  constexpr int KS = 64, XR = KS + 8, RB = 128 * AN, TB = 32 * BT;
+  __shared__ __attribute__((aligned(16))) half_t xs[2][TB * XR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int total = n_row * n_tok * ksn, L = blockIdx.x;
+  const int per = total / 8, rem = total % 8, xcd = L % 8;
+  const int idx = xcd * per + min(xcd, rem) + L / 8;
+  const int tok = idx % n_tok, rk = idx / n_tok, kz = rk % ksn, row = rk / ksn;
+  const int n0 = row * RB, t0 = tok * TB;
+  const int nall = K / KS, sbeg = kz * nall / ksn, nsteps = (kz + 1) * nall / ksn - sbeg;
+
+  const __amdgpu_buffer_rsrc_t wrs = w8_rsrc(w8 + static_cast<int64_t>(n0) * ldw + static_cast<int64_t>(sbeg) * KS);
+  const __amdgpu_buffer_rsrc_t xrs = w8_rsrc(x + static_cast<int64_t>(sbeg) * KS);
+  int woff[AN];
+#pragma unroll
+  for (int a = 0; a < AN; ++a)
+    woff[a] = (min(n0 + 32 * (AN * w + a) + c, N - 1) - n0) * static_cast<int>(ldw) + 32 * h;
+  int xoff[BT];  // activation piece j of this thread: token e / 8, k piece e % 8, e = tid + 256 j
+#pragma unroll
+  for (int j = 0; j < BT; ++j) {
+    const int e = tid + 256 * j, t = min(t0 + e / 8, T - 1);
+    xoff[j] = (t * K + 8 * (e % 8)) * 2;
+  }
+  uint4v wa[AN][2], wb[AN][2];
+  uint4v xr[BT];
+  auto load_w = [&](uint4v (&wr)[AN][2], int s) {
+    const int so = min(s, nsteps - 1) * KS;
+#pragma unroll
+    for (int a = 0; a < AN; ++a)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) wr[a][v] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[a] + 16 * v, so, 0);
+  };
+  auto load_x = [&](int s) {
+    const int so = min(s, nsteps - 1) * KS * 2;
+#pragma unroll
+    for (int j = 0; j < BT; ++j) xr[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[j], so, 0);
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const int e = tid + 256 * j;
+      *reinterpret_cast<uint4v*>(&xs[buf][(e / 8) * XR + 8 * (e % 8)]) = xr[j];
+    }
+  };
+  float16v acc[AN][BT];
+#pragma unroll
+  for (int a = 0; a < AN; ++a)
+#pragma unroll
+    for (int b = 0; b < BT; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+
+  auto compute = [&](const uint4v (&wr)[AN][2], int buf) {
+    const half_t* xb = &xs[buf][c * XR + 32 * h];
+    half8 bq[2][BT], av[2][AN];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) bq[0][b] = *reinterpret_cast<const half8*>(xb + 32 * b * XR);
+#pragma unroll
+    for (int a = 0; a < AN; ++a) av[0][a] = int8x8_to_half8_w8(wr[a][0][0], wr[a][0][1]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cu = q & 1, nx = cu ^ 1;
+      if (q < 3) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) bq[nx][b] = *reinterpret_cast<const half8*>(xb + 32 * b * XR + 8 * (q + 1));
+#pragma unroll
+        for (int a = 0; a < AN; ++a)
+          av[nx][a] = int8x8_to_half8_w8(wr[a][(q + 1) >> 1][2 * ((q + 1) & 1)], wr[a][(q + 1) >> 1][2 * ((q + 1) & 1) + 1]);
+      }
+#pragma unroll
+      for (int a = 0; a < AN; ++a)
+#pragma unroll
+        for (int b = 0; b < BT; ++b) acc[a][b] = mfma32x32x16(av[cu][a], bq[cu][b], acc[a][b]);
+    }
+  };
+  // Step s issues x(s + 1), computes s, then issues W(s + 2) into the set s just used.
+  // The loop has one back edge and no exit in its body (an exit there made the compiler
+  // keep two copies of the accumulators); an odd last step runs after it.
+  load_x(0);
+  load_w(wa, 0);
+  load_w(wb, 1);
+  stage(0);
+  __syncthreads();
+  int s = 0;
+  for (; s + 1 < nsteps; s += 2) {
+    load_x(s + 1);
+    compute(wa, 0);
+    load_w(wa, s + 2);
+    stage(1);
+    __syncthreads();
+    load_x(s + 2);
+    compute(wb, 1);
+    load_w(wb, s + 3);
+    stage(0);
+    __syncthreads();
+  }
+  if (s < nsteps) compute(wa, 0);
+
+  // Register 4 q + r of block (a, b) in lane (c, h): row 32 (AN w + a) + 8 q + 4 h + r,
+  // token 32 b + c.
+#pragma unroll
+  for (int b = 0; b < BT; ++b) {
+    const int t = t0 + 32 * b + c;
+    if (t >= T) continue;
+#pragma unroll
+    for (int a = 0; a < AN; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 32 * (AN * w + a) + 8 * q + 4 * h;
+        if (n >= N) continue;
+        float4v v = {acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]};
+        if (ksn > 1) {  // the host requires N % 4 == 0 here
+          *reinterpret_cast<float4v*>(ws + (static_cast<int64_t>(kz) * T + t) * N + n) = v;
+        } else if (vec_out && n + 3 < N) {
+          const float4v sc = {scale[n], scale[n + 1], scale[n + 2], scale[n + 3]};
+          float* yp = y + static_cast<int64_t>(t) * N + n;
+          v = v * sc;
+          if (beta != 0.0f) v += beta * *reinterpret_cast<const float4v*>(yp);
+          *reinterpret_cast<float4v*>(yp) = v;
+        } else {
+          float* yp = y + static_cast<int64_t>(t) * N;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) {
+              const float o = v[r] * scale[n + r];
+              yp[n + r] = o + (beta != 0.0f ? beta * yp[n + r] : 0.0f);
+            }
+        }
+      }
+  }
+}
+
+// Tiles: 128 rows x 128 tokens (3 waves per SIMD fit), or 256 x 96 (2 per SIMD) when the
+// grid already has >= 768 of the smaller tiles (28672 x 4096 at T = 560: 183 -> 167 us).
+struct W8TilePlan {
+  bool big;
+  int ksplit;
+};
+
+W8TilePlan w8_tile_plan(int T, int K, int N) {
+  const int small = ((N + 127) / 128) * ((T + 127) / 128);
+  if (small >= 768) return {true, 1};
+  // K ranges until the grid has >= 480 workgroups (about two per CU), at most 8 and each
+  // at least 4 steps of 64 k (measured at Llama-3-8B and TinyLlama shapes, T = 128-560).
+  int ks = small >= 384 ? 1 : std::min(8, (480 + small - 1) / small);
+  while (ks > 1 && (K / 64) / ks < 4) --ks;
+  if (N % 4) ks = 1;
+  return {false, ks};
+}
+
+template <int AN, int BT, int WPE>
+int launch_w8_tile(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K, int N,
+                   float beta, hipStream_t s, int ksplit, float* ws) {
+  const int n_row = (N + 128 * AN - 1) / (128 * AN), n_tok = (T + 32 * BT - 1) / (32 * BT);
+  const int64_t total = static_cast<int64_t>(n_row) * n_tok * ksplit;
+  RH_REQUIRE(total < (int64_t(1) << 31), "gemm_w8: grid too large");
+  const int vec_out = N % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((w8_tile_kernel<AN, BT, WPE>), dim3(static_cast<unsigned>(total)), dim3(256), 0, s,
+                                   w8, ldw, scale, x, y, T, K, N, beta, ws, n_row, n_tok, ksplit, vec_out));
+  if (ksplit > 1) {
+    const int64_t quads = static_cast<int64_t>(T) * N / 4;
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_split_merge_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                                     s, ws, ksplit, T, N, scale, y, beta));
+  }
+  return 0;
+}
+
 // The tile for 17-64 tokens: 128 rows x 64 tokens, 4 waves of 32 rows (the 128-token tile
 // leaves most MFMA columns idle there and gives 4x fewer row tiles per token).
 constexpr int kSkinnyRows = 128, kSkinnyTokens = 64;
@@ -252,16 +455,44 @@ constexpr int kSkinnyRows = 128, kSkinnyTokens = 64;
 using namespace relay_hip;
 
 
-extern "C" int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K,
-                          int N, float beta, void* stream) {
-  if (T == 0) return 0;
+static int gemm_w8_checks(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N) {
   RH_REQUIRE(T > 0 && N > 0 && K > 0 && K % 64 == 0, "gemm_w8: K must be a positive multiple of 64");
   RH_REQUIRE(ldw >= K && ldw % 16 == 0, "gemm_w8: ldw must be >= K and a multiple of 16");
   RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
              "gemm_w8: W8 and x must be 16-byte aligned");
+  RH_REQUIRE(static_cast<int64_t>(T) * K < (int64_t(1) << 30) && 256 * ldw < (int64_t(1) << 31),
+             "gemm_w8: T * K or the row stride too large for 32-bit buffer offsets");
+  return 0;
+}
+
+extern "C" int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K,
+                          int N, float beta, void* stream) {
+  if (T == 0) return 0;
+  if (int rc = gemm_w8_checks(w8, ldw, x, T, K, N)) return rc;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
-  return launch_w8<2, 2, 1, 2, 64, 1>(w8, ldw, scale, xh, y, T, K, N, beta, st);
+  if (w8_tile_plan(T, K, N).big) return launch_w8_tile<2, 3, 2>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
+  return launch_w8_tile<1, 4, 3>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
+}
+
+extern "C" int rh_gemm_w8_plan(int T, int K, int N) {
+  if (T < 1 || K <= 0 || K % 64 || N <= 0) return -1;
+  return w8_tile_plan(T, K, N).ksplit;
+}
+
+extern "C" int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T,
+                                int K, int N, float beta, int ksplit, float* workspace, void* stream) {
+  if (T == 0) return 0;
+  if (int rc = gemm_w8_checks(w8, ldw, x, T, K, N)) return rc;
+  RH_REQUIRE(ksplit >= 1 && ksplit <= kMaxW8Split && ksplit <= K / 64,
+             "gemm_w8_split: ksplit must be in 1..8 and at most the number of 64-k steps");
+  RH_REQUIRE(ksplit == 1 || workspace, "gemm_w8_split: ksplit > 1 needs a workspace");
+  RH_REQUIRE(ksplit == 1 || N % 4 == 0, "gemm_w8_split: ksplit > 1 needs N a multiple of 4");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const half_t* xh = static_cast<const half_t*>(x);
+  if (ksplit == 1 && w8_tile_plan(T, K, N).big)
+    return launch_w8_tile<2, 3, 2>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
+  return launch_w8_tile<1, 4, 3>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
 }
 
 // k per step of the skinny tile: 128 when K allows (measured 10-15% faster than 64 at

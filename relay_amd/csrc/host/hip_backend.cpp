@@ -234,7 +234,7 @@ class HipBackend final : public Backend {
   DeviceArray<std::uint16_t> kc_, vc_;
   DeviceArray<float> x_, qkv_, gu_, logits_;
   DeviceArray<std::uint16_t> xn_, qh_, attn_, act_;
-  DeviceArray<std::uint16_t> dequant_;  // int8 weights widened for a batch above the GEMV's limit
+  DeviceArray<std::uint16_t> dequant_;  // int8 weights widened (K % 64 != 0, above the GEMV's limit)
   std::size_t dequant_elems_ = 0;
   DeviceArray<float> stage_;            // fp32 staging for uploads and update_weight
 
@@ -332,7 +332,7 @@ DeviceMatrix HipBackend::make_matrix(const float* host, int N, int K, const Weig
                                 m.scale.p + r0, stream_));
     });
   }
-  dequant_elems_ = std::max(dequant_elems_, n);
+  if (K % 64) dequant_elems_ = std::max(dequant_elems_, n);  // the int8 GEMM needs K % 64 == 0
   return m;
 }
 
@@ -360,7 +360,8 @@ void HipBackend::load_weights(const WeightSource& src) {
     layers_.push_back(std::move(d));
   }
   HIP_CHECK(hipStreamSynchronize(stream_));
-  if (opt_.int8_weights && max_tokens_ > rh_gemv_int8_max_tokens()) dequant_ = DeviceArray<std::uint16_t>(dequant_elems_);
+  if (opt_.int8_weights && max_tokens_ > rh_gemv_int8_max_tokens() && dequant_elems_)
+    dequant_ = DeviceArray<std::uint16_t>(dequant_elems_);
   stage_ = DeviceArray<float>();  // uploads are done; update_weight reallocates on demand
 }
 
@@ -414,11 +415,11 @@ bool HipBackend::fused(const DeviceMatrix& W, int T, bool int8_ok) const {
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
   // int8 (measured at Llama-3-8B shapes): the GEMV up to 16 tokens; the split-K int8 GEMM
-  // at 17-64 tokens on wide or long-K matrices; the int8 GEMM for wide matrices
-  // (N >= 16384) up to 256 tokens (3.5x faster than dequantize + GEMM at T = 48); the GEMV
-  // up to 64 tokens on narrower ones; otherwise dequantize + library GEMM (relay's path for
-  // every T above its GEMV limit), which wins once the GEMM is compute-bound.
-  const bool wide = W.N >= 16384 && W.K % 64 == 0 && T <= 256;
+  // at 17-64 tokens on wide or long-K matrices; the GEMV up to 64 tokens on narrower ones;
+  // above 64 tokens the large-tile int8 GEMM with its K split (T = 560: 370 us per
+  // Llama-3-8B layer against 455 us for dequantize + library GEMM, relay's path for every
+  // T above its GEMV limit). Dequantize + library GEMM remains only for K not a multiple
+  // of 64.
   // 17-64 tokens on wide or long-K matrices: the int8 GEMM with the 64-token tile and K cut
   // into ranges (Llama-3-8B at T = 48: gate_up 64.9 -> 44.2 us, down 47.2 -> 28.6 us); the
   // GEMV stays ahead on the 4096-6144-row, K = 4096 matrices.
@@ -429,12 +430,15 @@ void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, i
     RH_CHECK(rh_gemm_w8_skinny(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, split_ws_.p, stream_));
     return;
   }
-  if (T <= 16 || (T <= rh_gemv_int8_max_tokens() && !wide)) {
+  if (T <= rh_gemv_int8_max_tokens()) {
     RH_CHECK(rh_gemv_int8(W.i8.p, W.ldw, W.scale.p, 0, x, y, T, W.K, W.N, beta, stream_));
     return;
   }
-  if (wide) {
-    RH_CHECK(rh_gemm_w8(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, stream_));
+  if (W.K % 64 == 0) {
+    const int ks = rh_gemm_w8_plan(T, W.K, W.N);
+    const std::size_t need = static_cast<std::size_t>(ks) * T * W.N;
+    if (ks > 1 && need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
+    RH_CHECK(rh_gemm_w8_split(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, split_ws_.p, stream_));
     return;
   }
   RH_CHECK(rh_dequant_int8(W.i8.p, W.ldw, W.scale.p, W.N, W.K, dequant_.p, stream_));

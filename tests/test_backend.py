@@ -240,7 +240,7 @@ def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev):
     logits may differ only by fp32 summation order (amplified where an activation is rounded
     to fp16 between layers: measured 2e-4; a wrong product would be off by O(1)). intermediate 8192 and 20 decode
     sequences put gate_up (N 16384) and down (K 8192) on the split-K int8 GEMM at 20
-    tokens; the prompts (100 tokens) take the dequantize + library GEMM path."""
+    tokens; the prompts (100 tokens) take the large-tile int8 GEMM with its K split."""
     w = small_model(64, 4, 2, layers=1, hidden=256, inter=8192, vocab=512, seed=3)
     rng = np.random.default_rng(11)
     for L in w.layers:

@@ -5,7 +5,7 @@ so the error is the fp32 accumulation over K terms plus the rounding of the scal
 (and of the beta term): |y - y_exact| <= (4 K 2^-24 + 2^-23) |scale[n]| sum_k |q x| (+ 2^-23
 |beta y|). The exact value is computed in float64 from the same int8/fp16 values (numpy as
 the checker). Sizes cover partial token and row tiles, T above and below the GEMV limit, and
-the shapes of the Llama-3-8B mixed batch (T = 560).
+the shapes of the Llama-3-8B mixed batch (T = 560), and the K-split form (rh_gemm_w8_split).
 """
 import numpy as np
 import pytest
@@ -42,7 +42,28 @@ def run(torch, dev, q, scale, x, beta=0.0, y0=None, ldw=None):
     return Y.cpu().numpy()
 
 
-def check(y, q, scale, x, beta=0.0, y0=None):
+def run_split(torch, dev, q, scale, x, ks):
+    from relay_amd import _lib
+
+    N, K = q.shape
+    T = x.shape[0]
+    W = torch.from_numpy(q).to(dev)
+    S = torch.from_numpy(scale).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    Y = torch.full((T, N), float("nan"), device=dev)
+    ws = torch.full((ks * T * N,), float("nan"), device=dev)
+    print(f"gemm_w8_split case: T={T} K={K} N={N} ksplit={ks}", flush=True)
+    _lib.check(_lib.lib().rh_gemm_w8_split(W.data_ptr(), K, S.data_ptr(), X.data_ptr(), Y.data_ptr(), T, K, N, 0.0, ks,
+                                           ws.data_ptr(), None), "rh_gemm_w8_split")
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+def check(y, q, scale, x, beta=0.0, y0=None, rows=None):
+    """rows: check only these output rows n (float64 over all of a large matrix is slow)."""
+    if rows is not None:
+        y, q, scale = y[:, rows], q[rows], scale[rows]
+        y0 = None if y0 is None else y0[:, rows]
     qd, xd, sd = q.astype(np.float64), x.astype(np.float64), scale.astype(np.float64)
     dot = xd @ qd.T
     mag = (np.abs(xd) @ np.abs(qd).T) * np.abs(sd)
@@ -66,6 +87,41 @@ def test_matches_float64(torch_mod, dev, T, N, K):
 def test_llama3_shapes_at_the_mixed_batch(torch_mod, dev, N, K):
     q, s, x = make(N, K, 560, seed=N + K)
     check(run(torch_mod, dev, q, s, x), q, s, x)
+
+
+def test_wide_matrix_at_the_mixed_batch(torch_mod, dev):
+    """Llama-3-8B's gate_up (28672 x 4096) at T = 560 runs the 256 x 96 tile; 1536 rows
+    spread over the matrix are checked against float64."""
+    q, s, x = make(28672, 4096, 560, seed=7)
+    rows = np.sort(np.random.default_rng(8).choice(28672, 1536, replace=False))
+    check(run(torch_mod, dev, q, s, x), q, s, x, rows=rows)
+
+
+@pytest.mark.parametrize("ks", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("T,N,K", [(300, 576, 1536), (65, 256, 4096), (129, 1000, 5632), (560, 4096, 1024)])
+def test_split_matches_float64(torch_mod, dev, ks, T, N, K):
+    """rh_gemm_w8_split: K cut into 1-8 ranges (a range of 2 steps at K = 1024, ks = 8),
+    ranges added in order by the merge launch."""
+    q, s, x = make(N, K, T, seed=T + N + K + ks)
+    check(run_split(torch_mod, dev, q, s, x, ks), q, s, x)
+
+
+def test_split_is_deterministic(torch_mod, dev):
+    q, s, x = make(512, 4096, 200, seed=9)
+    a = run_split(torch_mod, dev, q, s, x, 4)
+    b = run_split(torch_mod, dev, q, s, x, 4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_plan(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    # Llama-3-8B at config 5's 560 tokens: qkv, wo, gate_up, down
+    assert [L.rh_gemm_w8_plan(560, k, n) for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))] == \
+        [2, 3, 1, 3]
+    assert L.rh_gemm_w8_plan(560, 100, 64) == -1 and L.rh_gemm_w8_plan(0, 64, 64) == -1
+    assert 1 <= L.rh_gemm_w8_plan(100, 128, 4096) <= 2  # ranges of at least 4 steps of 64 k
 
 
 def test_beta_accumulates(torch_mod, dev):
@@ -108,6 +164,11 @@ def test_rejects_bad_shapes(torch_mod, dev):
     assert L.rh_gemm_w8(None, 96, None, None, None, 4, 96, 64, 0.0, None) != 0 and "K must" in _lib.last_error()
     assert L.rh_gemm_w8(None, 72, None, None, None, 4, 64, 64, 0.0, None) != 0 and "ldw" in _lib.last_error()
     assert L.rh_gemm_w8(None, 64, None, None, None, 0, 64, 64, 0.0, None) == 0  # nothing to do
+    assert L.rh_gemm_w8_split(None, 64, None, None, None, 4, 64, 64, 0.0, 2, None, None) != 0  # 2 ranges of 1 step
+    assert "ksplit" in _lib.last_error()
+    assert L.rh_gemm_w8_split(None, 128, None, None, None, 4, 128, 64, 0.0, 2, None, None) != 0
+    assert "workspace" in _lib.last_error()
+    assert L.rh_gemm_w8_split(None, 128, None, None, None, 4, 128, 66, 0.0, 2, None, None) != 0
 
 
 def run_skinny(torch, dev, q, scale, x, ks, beta=0.0, y0=None, ldw=None):

@@ -67,3 +67,17 @@ def test_random_products(torch_mod, dev, seed):
     print(f"random int8 split GEMM {seed}: T {T} N {N} K {K} ksplit {ks}", flush=True)
     q, sc, x = TW.make(N, K, T, seed=seed)
     TW.check(TW.run_skinny(torch_mod, dev, q, sc, x, ks), q, sc, x)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_large_batch_int8(torch_mod, dev, seed):
+    """The large-batch int8 GEMM (rh_gemm_w8 and its K split) over random T above the GEMV
+    limit, N (any, or a multiple of 4 for a split) and K (a multiple of 64)."""
+    rng = np.random.default_rng(4000 + seed)
+    T, K = int(rng.integers(65, 700)), 64 * int(rng.integers(1, 80))
+    ks = int(rng.integers(1, min(8, K // 64) + 1))
+    N = int(rng.integers(1, 3000)) * (4 if ks > 1 else 1)
+    print(f"random int8 large-batch GEMM {seed}: T {T} N {N} K {K} ksplit {ks}", flush=True)
+    q, sc, x = TW.make(N, K, T, seed=seed)
+    y = TW.run_split(torch_mod, dev, q, sc, x, ks) if ks > 1 else TW.run(torch_mod, dev, q, sc, x)
+    TW.check(y, q, sc, x)
