@@ -162,7 +162,8 @@ int64_t rh_gemv_int8_row_stride(int K);
 /* Largest T rh_gemv_int8 takes. */
 int rh_gemv_int8_max_tokens(void);
 
-/* rh_gemv_int8 with the producer of x or qkv_post folded in, for 1 <= T <= 16 (no
+/* rh_gemv_int8 with the producer of x or qkv_post folded in, for 1 <= T <= 16 (1 <= T <= 32
+ * for rh_gemv_int8_qkv, which folds in only qkv_post) (no
  * counterpart in relay, where rms_norm_kernel, silu_mul_kernel and qkv_post run as their own
  * launches around the GEMV, cuda_backend.cu:575-591): the int8 counterparts of
  * rh_gemv_f16_rmsnorm, rh_gemv_f16_silu, rh_gemv_f16_qkv and rh_gemv_f16_rmsnorm_qkv, with
@@ -262,13 +263,11 @@ int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const vo
                      int N, float beta, int ksplit, float* workspace, void* stream);
 int rh_gemm_w8_plan(int T, int K, int N);
 
-/* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 64-token tile and K cut into ksplit ranges
- * (1 <= ksplit <= 8, at most one per step of 128 k, or of 64 k when K is not a multiple
- * of 128), so that decode batches of 17-64 tokens read the int8
- * weights once on enough workgroups. ksplit > 1 writes each range's raw sums to workspace
- * (fp32, ksplit * T * N values, N a multiple of 4) and a second launch adds them in range
- * order before the scale and beta (deterministic). Calls sharing a workspace must not
- * overlap. No counterpart in relay (dequantize + cublasGemmEx, cuda_backend.cu:718-722). */
+/* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 32-token tile (64 tokens above 32) and K cut
+ * into ksplit ranges (1 <= ksplit <= 8, at most K / 64), so that decode batches of 17-64
+ * tokens read the int8 weights once on enough workgroups; workspace as for
+ * rh_gemm_w8_split. No counterpart in relay (dequantize + cublasGemmEx,
+ * cuda_backend.cu:718-722). */
 int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
                       float beta, int ksplit, float* workspace, void* stream);
 

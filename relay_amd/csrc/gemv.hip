@@ -295,8 +295,8 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_kernel(const int8_t* 
   constexpr int U = NB == 1 ? (RT <= 2 ? kUnroll : 2) : (NB == 2 ? 2 : 1);
   __shared__ float red[WAVES][RT][NB][kWave * 4];
   __shared__ float s_inv[PRO == kRmsNorm ? kMaxTokens : 1];
-  __shared__ int s_pos[EPI == kRope ? kMaxTokens : 1];
-  __shared__ int64_t s_kvrow[EPI == kRope ? kMaxTokens : 1];
+  __shared__ int s_pos[EPI == kRope ? NB * kMaxTokens : 1];
+  __shared__ int64_t s_kvrow[EPI == kRope ? NB * kMaxTokens : 1];
   extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // PRO != kPlain: [T][K + 8]
   const half_t* x = static_cast<const half_t*>(xin);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -798,6 +798,19 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
   // Fused launches keep the 16-row tile at 1-8 tokens too (a one-token vector-ALU form
   // behind the producers made TinyLlama int8 decode steps slower).
   const int tiles = (N + 15) / 16;
+  if constexpr (PRO == kPlain) {
+    if (T > kMaxTokens) {  // the qkv epilogue alone, 17-32 tokens: two column blocks
+      if (tiles < 256) {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 2, 1, F16_SCALE, PRO, EPI>), dim3(tiles),
+                                         dim3(16 * kWave), 0, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16,
+                                         ra));
+      } else {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, 2, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(8 * kWave),
+                                         0, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16, ra));
+      }
+      return 0;
+    }
+  }
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(16 * kWave),
                                      staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16, ra));
@@ -808,8 +821,10 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
   return 0;
 }
 
-int check_int8_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x, int T, int K, int N) {
-  RH_REQUIRE(T >= 1 && T <= kMaxTokens, "gemv_int8 fused: T must be in 1..16");
+int check_int8_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x, int T, int K, int N,
+                     int max_t = kMaxTokens) {
+  RH_REQUIRE(T >= 1 && T <= max_t, max_t == kMaxTokens ? "gemv_int8 fused: T must be in 1..16"
+                                                       : "gemv_int8 fused: T must be in 1..32");
   RH_REQUIRE(K > 0 && N > 0 && K % 16 == 0, "gemv_int8: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
              "gemv_int8: ldw must be >= K, < 2^21 and a multiple of 16");
@@ -832,7 +847,7 @@ template <int PRO, int EPI>
 int int8_fused(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* xin,
                const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream,
                const RopeArgs& ra = RopeArgs{}) {
-  if (int rc = check_int8_fused(w8, ldw, scale, xin, T, K, N)) return rc;
+  if (int rc = check_int8_fused(w8, ldw, scale, xin, T, K, N, PRO == kPlain ? 2 * kMaxTokens : kMaxTokens)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return scale_is_f16 ? launch_fused<true, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra)
                       : launch_fused<false, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra);

@@ -208,6 +208,7 @@ class HipBackend final : public Backend {
   void gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta);
   // int8_ok: the caller has an int8 variant of the fused product (the qkv projection).
   bool fused(const DeviceMatrix& W, int T, bool int8_ok = false) const;
+  float* w8_split_ws(int ks, int T, int N);
   void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
   // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
   static bool skinny(int K, int N, int T);
@@ -412,6 +413,14 @@ bool HipBackend::fused(const DeviceMatrix& W, int T, bool int8_ok) const {
          rh_gemv_f16_fused_fits(T, W.K);
 }
 
+// The K-range workspace of a split int8 product (grown on demand).
+float* HipBackend::w8_split_ws(int ks, int T, int N) {
+  if (ks <= 1) return nullptr;
+  const std::size_t need = static_cast<std::size_t>(ks) * T * N;
+  if (need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
+  return split_ws_.p;
+}
+
 void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, int T, float beta) {
   if (!W.i8.p) return gemm_f16(W.f16.p, x, y, T, W.K, W.N, beta);
   // int8 (measured at Llama-3-8B shapes): the GEMV up to 16 tokens; the split-K int8 GEMM
@@ -420,14 +429,13 @@ void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, i
   // Llama-3-8B layer against 455 us for dequantize + library GEMM, relay's path for every
   // T above its GEMV limit). Dequantize + library GEMM remains only for K not a multiple
   // of 64.
-  // 17-64 tokens on wide or long-K matrices: the int8 GEMM with the 64-token tile and K cut
-  // into ranges (Llama-3-8B at T = 48: gate_up 64.9 -> 44.2 us, down 47.2 -> 28.6 us); the
-  // GEMV stays ahead on the 4096-6144-row, K = 4096 matrices.
-  if (T > 16 && T <= 64 && W.K % 64 == 0 && W.N % 4 == 0 && (W.N >= 16384 || W.K >= 8192)) {
+  // 17-64 tokens on wide or long-K matrices: the int8 GEMM with the 32- or 64-token tile and
+  // K cut into ranges (T = 32: Llama-3-8B gate_up 32.8 us, down 24.3; TinyLlama gate_up 15.0
+  // against 15.7 for the GEMV, down 12.3 against 15.2); the GEMV stays ahead on matrices of
+  // K <= 4096 and <= 6144 rows (4096 x 4096 at T = 32: 12.5 against 13.5 us).
+  if (T > 16 && T <= 64 && W.K % 64 == 0 && W.N % 4 == 0 && (W.N >= 8192 || W.K >= 5000)) {
     const int ks = rh_gemm_w8_split_plan(T, W.K, W.N);
-    const std::size_t need = static_cast<std::size_t>(ks) * T * W.N;
-    if (ks > 1 && need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
-    RH_CHECK(rh_gemm_w8_skinny(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, split_ws_.p, stream_));
+    RH_CHECK(rh_gemm_w8_skinny(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, w8_split_ws(ks, T, W.N), stream_));
     return;
   }
   if (T <= rh_gemv_int8_max_tokens()) {
@@ -436,9 +444,7 @@ void HipBackend::gemm(const DeviceMatrix& W, const std::uint16_t* x, float* y, i
   }
   if (W.K % 64 == 0) {
     const int ks = rh_gemm_w8_plan(T, W.K, W.N);
-    const std::size_t need = static_cast<std::size_t>(ks) * T * W.N;
-    if (ks > 1 && need > split_ws_.n) split_ws_ = DeviceArray<float>(need);
-    RH_CHECK(rh_gemm_w8_split(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, split_ws_.p, stream_));
+    RH_CHECK(rh_gemm_w8_split(W.i8.p, W.ldw, W.scale.p, x, y, T, W.K, W.N, beta, ks, w8_split_ws(ks, T, W.N), stream_));
     return;
   }
   RH_CHECK(rh_dequant_int8(W.i8.p, W.ldw, W.scale.p, W.N, W.K, dequant_.p, stream_));
@@ -587,9 +593,10 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
         RH_CHECK(rh_gemv_f16_rmsnorm_qkv(L.wqkv.f16.p, H, x_.p, L.attn_norm.p, eps, qkv_.p, T, H, bias, inv_freq_.p,
                                          d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads,
                                          D, layout_.block_size, stream_));
-    } else if (L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 && T <= 16 && (QKV + 15) / 16 <= 256) {
+    } else if (L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 && T <= 32 && (QKV + 15) / 16 <= 256) {
       // int8: the projection and qkv_post in one launch (its 16-row tiles in one round;
-      // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms).
+      // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms; at 17-32 tokens two 16-token
+      // column blocks).
       RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_int8_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, xn_.p, qkv_.p, T, H, bias, inv_freq_.p,
                                 d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D,

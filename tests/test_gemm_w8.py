@@ -195,7 +195,7 @@ def run_skinny(torch, dev, q, scale, x, ks, beta=0.0, y0=None, ldw=None):
 @pytest.mark.parametrize("T,N,K", [(1, 64, 1024), (17, 200, 2048), (48, 1000, 4096), (64, 4096, 14336 // 4),
                                    (33, 132, 1088)])
 def test_skinny_split_k_matches_float64(torch_mod, dev, T, N, K, ks):
-    """rh_gemm_w8_skinny at any K split (128-k steps, or 64 for K = 1088) stays within the
+    """rh_gemm_w8_skinny at any K split (ranges of whole 64-k steps) stays within the
     fp32 bound; the split adds the ranges in order, so a repeat gives the same bits."""
     q, scale, x = make(N, K, T, seed=T + N + K + ks)
     y = run_skinny(torch_mod, dev, q, scale, x, ks)
@@ -214,7 +214,7 @@ def test_skinny_accumulates_and_limits(torch_mod, dev):
     assert L.rh_gemm_w8_split_plan(65, 4096, 4096) == -1
     assert L.rh_gemm_w8_skinny(None, 128, None, None, None, 65, 128, 64, 0.0, 1, None, None) != 0
     assert "T must be in 1..64" in _lib.last_error()
-    assert L.rh_gemm_w8_skinny(None, 128, None, None, None, 8, 128, 64, 0.0, 2, None, None) != 0
+    assert L.rh_gemm_w8_skinny(None, 64, None, None, None, 8, 64, 64, 0.0, 2, None, None) != 0
     assert "ksplit" in _lib.last_error()
     assert L.rh_gemm_w8_skinny(None, 256, None, None, None, 8, 256, 64, 0.0, 2, None, None) != 0
     assert "workspace" in _lib.last_error()

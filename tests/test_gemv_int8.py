@@ -250,7 +250,8 @@ def f16_close(a_bits, b_bits, tol, name):
 @pytest.mark.parametrize("T,heads,kvh,D,H,bs,with_bias,norm", [
     (1, 9, 3, 64, 576, 16, False, True), (15, 32, 4, 64, 2048, 16, True, False), (5, 16, 8, 128, 4096, 16, False, True),
     (8, 8, 2, 64, 320, 12, True, True), (3, 4, 4, 16, 64, 1, True, True), (16, 32, 4, 64, 2048, 16, False, False),
-    (2, 16, 4, 128, 2048, 16, False, False)])
+    (2, 16, 4, 128, 2048, 16, False, False), (24, 32, 4, 64, 2048, 16, True, False),
+    (32, 32, 4, 64, 2048, 16, False, False), (17, 8, 2, 128, 512, 16, True, False)])
 def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, with_bias, norm):
     """rh_gemv_int8_rmsnorm_qkv (norm) or rh_gemv_int8_qkv (x already normalised) against
     rh_rmsnorm -> rh_gemv_int8 -> rh_qkv_post. Without rotation (inv_freq = 0) every byte of
