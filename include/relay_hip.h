@@ -271,6 +271,28 @@ int rh_gemm_w8_plan(int T, int K, int N);
 int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,
                       float beta, int ksplit, float* workspace, void* stream);
 
+/* The first half of a split int8 product, for consumers that merge it themselves: the raw
+ * sums of ksplit K ranges (2 <= ksplit <= 8, at most K / 64) into workspace [ksplit][T][N]
+ * (N a multiple of 4), with the tile rh_gemm_w8_skinny (T <= 64) or rh_gemm_w8_split takes
+ * at this T; no scale is applied. The merges below then add the ranges in order and apply
+ * the scale, with the arithmetic of the two-launch chain (same bits). */
+int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N, int ksplit,
+                        float* workspace, void* stream);
+
+/* act[t, i] = silu(g) * up of the merged gate_up partials (rows [0, I) gate, [I, 2I) up;
+ * act fp16 [T, I], I a multiple of 8): rh_gemm_w8_skinny's merge followed by rh_silu_mul in
+ * one launch (relay: silu_mul_kernel after the GEMM, cuda_backend.cu:588-589). */
+int rh_w8_merge_silu(const float* workspace, int ksplit, int T, int I, const float* scale, void* act, void* stream);
+
+/* x[t] += merged partials (beta = 1), then out = RMSNorm(x[t]) * norm_w (fp16 [T, H]): a
+ * residual projection's merge, the residual add and the following RMSNorm in one launch,
+ * with rh_rmsnorm's arithmetic (relay: rmsnorm_kernel after the GEMM, cuda_backend.cu:575,
+ * 586-587). Also serves the o projection and the MLP's RMSNorm. H must satisfy rh_w8_merge_rmsnorm_fits (a multiple of 4, at
+ * most 4096). */
+int rh_w8_merge_rmsnorm(const float* workspace, int ksplit, int T, int H, const float* scale, float* x,
+                        const float* norm_w, float eps, void* out, void* stream);
+int rh_w8_merge_rmsnorm_fits(int H);
+
 /* The ksplit rh_gemm_w8_skinny uses for this shape (-1 outside its limits). */
 int rh_gemm_w8_split_plan(int T, int K, int N);
 

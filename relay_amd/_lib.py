@@ -70,6 +70,10 @@ SIGNATURES = {
     "rh_gemm_w8": (I, [P, I64, P, P, P, I, I, I, F, P]),
     "rh_gemm_w8_skinny": (I, [P, I64, P, P, P, I, I, I, F, I, P, P]),
     "rh_gemm_w8_split": (I, [P, I64, P, P, P, I, I, I, F, I, P, P]),
+    "rh_gemm_w8_partials": (I, [P, I64, P, I, I, I, I, P, P]),
+    "rh_w8_merge_silu": (I, [P, I, I, I, P, P, P]),
+    "rh_w8_merge_rmsnorm": (I, [P, I, I, I, P, P, P, F, P, P]),
+    "rh_w8_merge_rmsnorm_fits": (I, [I]),
     "rh_gemm_w8_plan": (I, [I, I, I]),
     "rh_gemm_w8_split_plan": (I, [I, I, I]),
     "rh_gemv_f16_rmsnorm": (I, [P, I64, P, P, F, P, I, I, I, F, P]),

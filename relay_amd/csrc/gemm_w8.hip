@@ -265,13 +265,16 @@ W8TilePlan w8_tile_plan(int T, int K, int N) {
 template <int AN, int BT, int WPE>
 int launch_w8_tile(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K, int N,
                    float beta, hipStream_t s, int ksplit, float* ws) {
+  // ksplit < 0: -ksplit ranges, partials only (no merge launch; a fused consumer merges).
+  const bool merge = ksplit > 0;
+  ksplit = merge ? ksplit : -ksplit;
   const int n_row = (N + 128 * AN - 1) / (128 * AN), n_tok = (T + 32 * BT - 1) / (32 * BT);
   const int64_t total = static_cast<int64_t>(n_row) * n_tok * ksplit;
   RH_REQUIRE(total < (int64_t(1) << 31), "gemm_w8: grid too large");
   const int vec_out = N % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
   RH_TRY_LAUNCH(hipLaunchKernelGGL((w8_tile_kernel<AN, BT, WPE>), dim3(static_cast<unsigned>(total)), dim3(256), 0, s,
                                    w8, ldw, scale, x, y, T, K, N, beta, ws, n_row, n_tok, ksplit, vec_out));
-  if (ksplit > 1) {
+  if (ksplit > 1 && merge) {
     const int64_t quads = static_cast<int64_t>(T) * N / 4;
     RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_split_merge_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
                                      s, ws, ksplit, T, N, scale, y, beta));
@@ -323,6 +326,21 @@ extern "C" int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scal
   if (ksplit == 1 && w8_tile_plan(T, K, N).big)
     return launch_w8_tile<2, 3, 2>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
   return launch_w8_tile<1, 4, 3>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
+}
+
+extern "C" int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N, int ksplit,
+                                   float* workspace, void* stream) {
+  if (T == 0) return 0;
+  if (int rc = gemm_w8_checks(w8, ldw, x, T, K, N)) return rc;
+  RH_REQUIRE(ksplit >= 2 && ksplit <= kMaxW8Split && ksplit <= K / 64 && workspace && N % 4 == 0,
+             "gemm_w8_partials: ksplit in 2..8 (at most K / 64), a workspace and N a multiple of 4");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const half_t* xh = static_cast<const half_t*>(x);
+  // No scale is read: the partials are the raw sums. The tile is the one the merging entry
+  // point takes for this T.
+  if (T <= 32) return launch_w8_tile<1, 1, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
+  if (T <= 64) return launch_w8_tile<1, 2, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
+  return launch_w8_tile<1, 4, 3>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
 }
 
 // 17-64 tokens: 128 rows x 32 tokens (x 64 above 32 tokens), four waves per SIMD, K cut

@@ -209,6 +209,7 @@ class HipBackend final : public Backend {
   // int8_ok: the caller has an int8 variant of the fused product (the qkv projection).
   bool fused(const DeviceMatrix& W, int T, bool int8_ok = false) const;
   float* w8_split_ws(int ks, int T, int N);
+  int w8_partials(const DeviceMatrix& W, const std::uint16_t* x, int T);
   void gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float* y, int T, int K, int N, float beta);
   // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
   static bool skinny(int K, int N, int T);
@@ -413,6 +414,22 @@ bool HipBackend::fused(const DeviceMatrix& W, int T, bool int8_ok) const {
          rh_gemv_f16_fused_fits(T, W.K);
 }
 
+// The K ranges of an int8 product that gemm() would split at this T, with its partials
+// written to split_ws_ for a consumer that merges them (rh_w8_merge_silu /
+// rh_w8_merge_rmsnorm, one launch fewer per product); 0 when gemm() does not split it.
+int HipBackend::w8_partials(const DeviceMatrix& W, const std::uint16_t* x, int T) {
+  if (!W.i8.p || T <= 16 || W.K % 64 || W.N % 4) return 0;
+  int ks = 0;
+  if (T <= 64) {
+    if (W.N >= 8192 || W.K >= 5000) ks = rh_gemm_w8_split_plan(T, W.K, W.N);
+  } else {
+    ks = rh_gemm_w8_plan(T, W.K, W.N);
+  }
+  if (ks < 2) return 0;
+  RH_CHECK(rh_gemm_w8_partials(W.i8.p, W.ldw, x, T, W.K, W.N, ks, w8_split_ws(ks, T, W.N), stream_));
+  return ks;
+}
+
 // The K-range workspace of a split int8 product (grown on demand).
 float* HipBackend::w8_split_ws(int ks, int T, int N) {
   if (ks <= 1) return nullptr;
@@ -577,6 +594,7 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
   const float q_scale = scale * 1.4426950408889634f, attn_scale = 0.6931471805599453f;
   HIP_CHECK(hipEventRecord(fwd_begin_, stream_));
   RH_CHECK(rh_embed(d_tok, T, embed_.p, H, x_.p, stream_));
+  bool attn_xn_ready = false;  // the previous layer's fused down merge wrote this layer's xn
   for (int l = 0; l < c_.layers; ++l) {
     DeviceLayer& L = layers_[l];
     std::uint16_t* kc = kc_.p + static_cast<std::size_t>(l) * layout_.layer_elems();
@@ -597,7 +615,7 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       // int8: the projection and qkv_post in one launch (its 16-row tiles in one round;
       // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms; at 17-32 tokens two 16-token
       // column blocks).
-      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      if (!attn_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_int8_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, xn_.p, qkv_.p, T, H, bias, inv_freq_.p,
                                 d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D,
                                 layout_.block_size, stream_));
@@ -606,11 +624,11 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       // (17-32 tokens: TinyLlama's 2560-row qkv 11.1 us here against 9.5 + 3.0 us for the
       // library product and a separate qkv_post.)
       // The projection and qkv_post in one launch (the RMSNorm cannot be folded in here).
-      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      if (!attn_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_f16_qkv(L.wqkv.f16.p, H, xn_.p, qkv_.p, T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab,
                                kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     } else {
-      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
+      if (!attn_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       gemm(L.wqkv, xn_.p, qkv_.p, T, 0.0f);
       // The fast kernels read only the fp16 q and the cache; the reference kernel reads qkv.
       if (q_out)
@@ -620,6 +638,7 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
         RH_CHECK(rh_qkv_post(qkv_.p, T, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, 1.0f,
                              c_.heads, c_.kv_heads, D, layout_.block_size, stream_));
     }
+    attn_xn_ready = false;
     HIP_CHECK(hipEventRecord(layer_done_[l], stream_));
     if (observer) observer->kv_written(l);
     if (fast_attention_) {
@@ -634,19 +653,44 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       RH_CHECK(rh_reference_attention(qkv_.p, QKV, kc, vc, d_pos, d_seq, d_toff, d_tab, nullptr, T, c_.heads,
                                       c_.kv_heads, D, layout_.block_size, scale, attn_.p, Q, stream_));
     }
-    gemm(L.wo, attn_.p, x_.p, T, 1.0f);  // x += attn W_o^T
+    // int8 products split over K (17+ tokens) leave their partials to the consumer: the o
+    // and down projections' merge, residual add and following RMSNorm run as one launch,
+    // the gate_up merge and SiLU as another (TinyLlama int8 32 x 2048 decode step: two
+    // launches fewer per layer).
+    bool mlp_xn_ready = false;
+    const bool merge_norm = rh_w8_merge_rmsnorm_fits(H);
+    if (const int ks = merge_norm ? w8_partials(L.wo, attn_.p, T) : 0) {
+      RH_CHECK(rh_w8_merge_rmsnorm(split_ws_.p, ks, T, H, L.wo.scale.p, x_.p, L.mlp_norm.p, eps, xn_.p, stream_));
+      mlp_xn_ready = true;
+    } else {
+      gemm(L.wo, attn_.p, x_.p, T, 1.0f);  // x += attn W_o^T
+    }
+    bool act_ready = false;
     if (fused(L.w_gate_up, T)) {
       RH_CHECK(rh_gemv_f16_rmsnorm(L.w_gate_up.f16.p, H, x_.p, L.mlp_norm.p, eps, gu_.p, T, H, 2 * I, 0.0f,
                                    stream_));
     } else {
-      RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
-      gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
+      if (!mlp_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
+      const int ks = I % 8 == 0 ? w8_partials(L.w_gate_up, xn_.p, T) : 0;
+      if (ks) {
+        RH_CHECK(rh_w8_merge_silu(split_ws_.p, ks, T, I, L.w_gate_up.scale.p, act_.p, stream_));
+        act_ready = true;
+      } else {
+        gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
+      }
     }
     if (fused(L.w_down, T)) {
       RH_CHECK(rh_gemv_f16_silu(L.w_down.f16.p, I, gu_.p, x_.p, T, I, H, 1.0f, stream_));  // x += act W_down^T
     } else {
-      RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
-      gemm(L.w_down, act_.p, x_.p, T, 1.0f);  // x += act W_down^T
+      if (!act_ready) RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
+      const int ks = merge_norm && l + 1 < c_.layers ? w8_partials(L.w_down, act_.p, T) : 0;
+      if (ks) {  // x += act W_down^T, then the next layer's attention RMSNorm
+        RH_CHECK(rh_w8_merge_rmsnorm(split_ws_.p, ks, T, H, L.w_down.scale.p, x_.p, layers_[l + 1].attn_norm.p, eps,
+                                     xn_.p, stream_));
+        attn_xn_ready = true;
+      } else {
+        gemm(L.w_down, act_.p, x_.p, T, 1.0f);  // x += act W_down^T
+      }
     }
   }
   if (R) {

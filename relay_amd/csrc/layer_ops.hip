@@ -133,6 +133,92 @@ __global__ void rmsnorm_vec_kernel(const float* x, const int* rows, const float*
   }
 }
 
+// ---- the K-range merge of a split int8 product, fused into its consumer ----------------
+//
+// rh_gemm_w8_partials leaves ksn raw partial planes ws[z][t][n]. The merge of a split product
+// (w8_split_merge_kernel) computes y = (sum_z ws[z]) * scale (+ beta y, the ranges added in
+// order); these kernels do that merge for the product's consumer in the same launch, with
+// the same arithmetic, so that a decode step saves the merge launch (~4.5 us at T = 32).
+
+constexpr int kMaxMergeSplit = 8;
+
+// The merged, scaled values of elements (t, n .. n + 3) (beta = 0: `+ 0.0f` keeps the
+// merge's sign of a zero result); every partial's 16-byte load issued before the adds.
+__device__ __forceinline__ float4 merged4(const float* ws, int ksn, int64_t plane, int64_t e, const float* sc) {
+  float4 p[kMaxMergeSplit];
+#pragma unroll
+  for (int z = 0; z < kMaxMergeSplit; ++z)
+    p[z] = z < ksn ? *reinterpret_cast<const float4*>(ws + z * plane + e) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int z = 0; z < kMaxMergeSplit; ++z)
+    if (z < ksn) v = float4{v.x + p[z].x, v.y + p[z].y, v.z + p[z].z, v.w + p[z].w};
+  return float4{v.x * sc[0], v.y * sc[1], v.z * sc[2], v.w * sc[3]};
+}
+
+// act = silu(gate) * up of the merged gate_up product (rows [0, I) gate, [I, 2I) up), the
+// arithmetic of silu_mul_vec_kernel; 8 elements per thread.
+__global__ void w8_merge_silu_kernel(const float* __restrict__ ws, int ksn, int T, int I,
+                                     const float* __restrict__ scale, half_t* act) {
+  const int t = blockIdx.x, i = (blockIdx.y * kThreads + threadIdx.x) * 8;
+  if (i >= I) return;
+  const int64_t plane = static_cast<int64_t>(T) * 2 * I, row = static_cast<int64_t>(t) * 2 * I;
+  const float4 g0 = merged4(ws, ksn, plane, row + i, scale + i), g1 = merged4(ws, ksn, plane, row + i + 4, scale + i + 4);
+  const float4 u0 = merged4(ws, ksn, plane, row + I + i, scale + I + i),
+               u1 = merged4(ws, ksn, plane, row + I + i + 4, scale + I + i + 4);
+  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  half8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float g = gv[e] + 0.0f, u = uv[e] + 0.0f;
+    r[e] = f16_of_product(g / (1.0f + expf(-g)), u);
+  }
+  *reinterpret_cast<half8*>(act + static_cast<int64_t>(t) * I + i) = r;
+}
+
+// x[t] += merged product (the merge's beta = 1), then out = RMSNorm(x[t]) * w in fp16: the
+// arithmetic and summation order of rmsnorm_vec_kernel (H % 4 == 0, H <= 4 kRmsVec kThreads).
+__global__ void w8_merge_rmsnorm_kernel(const float* __restrict__ ws, int ksn, int T, int H,
+                                        const float* __restrict__ scale, float* x, const float* __restrict__ w,
+                                        float eps, half_t* out) {
+  __shared__ double scratch[kThreads / 64];
+  const int r = blockIdx.x;
+  const int64_t plane = static_cast<int64_t>(T) * H, row = static_cast<int64_t>(r) * H;
+  float4* xr = reinterpret_cast<float4*>(x + row);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  const int n4 = H / 4;
+  float4 xv[kRmsVec], wv[kRmsVec];
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int j = threadIdx.x + i * kThreads;
+    if (j < n4) {
+      const float4 old = xr[j];
+      const float4 m = merged4(ws, ksn, plane, row + 4 * j, scale + 4 * j);
+      xv[i] = float4{m.x + old.x, m.y + old.y, m.z + old.z, m.w + old.w};
+      xr[j] = xv[i];
+      wv[i] = wr[j];
+    } else {
+      xv[i] = wv[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  double ss = 0;
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i)
+    ss += static_cast<double>(xv[i].x) * xv[i].x + static_cast<double>(xv[i].y) * xv[i].y +
+          static_cast<double>(xv[i].z) * xv[i].z + static_cast<double>(xv[i].w) * xv[i].w;
+  ss = block_sum(ss, scratch);
+  const float inv = 1.0f / sqrtf(static_cast<float>(ss / H) + eps);
+  half4* o = reinterpret_cast<half4*>(out + row);
+#pragma unroll
+  for (int i = 0; i < kRmsVec; ++i) {
+    const int j = threadIdx.x + i * kThreads;
+    if (j < n4)
+      o[j] = half4{f16_of_product(wv[i].x, xv[i].x * inv), f16_of_product(wv[i].y, xv[i].y * inv),
+                   f16_of_product(wv[i].z, xv[i].z * inv), f16_of_product(wv[i].w, xv[i].w * inv)};
+  }
+}
+
 // One thread per (token, head, pair (i, i + D/2)) of every head, grid (T, pieces): bias, then
 // RoPE on q and k heads, the fp32 row written back, and the fp16 copies (q to q_out, k and v
 // into the paged cache). Each element is touched by one thread, so no barriers.
@@ -441,6 +527,33 @@ int rh_silu_mul(const float* gu, int T, int I, void* act, void* stream) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL(silu_mul_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                                      gu, I, static_cast<half_t*>(act)));
   }
+  return 0;
+}
+
+int rh_w8_merge_silu(const float* workspace, int ksplit, int T, int I, const float* scale, void* act, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && I > 0 && I % 8 == 0 && ksplit >= 1 && ksplit <= kMaxMergeSplit,
+             "w8_merge_silu: I must be a positive multiple of 8 and ksplit in 1..8");
+  RH_REQUIRE(workspace && scale && act && reinterpret_cast<uintptr_t>(act) % 16 == 0, "w8_merge_silu: bad pointer");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_merge_silu_kernel, dim3(T, (I + 8 * kThreads - 1) / (8 * kThreads)),
+                                   dim3(kThreads), 0, static_cast<hipStream_t>(stream), workspace, ksplit, T, I, scale,
+                                   static_cast<half_t*>(act)));
+  return 0;
+}
+
+int rh_w8_merge_rmsnorm_fits(int H) { return H > 0 && H % 4 == 0 && H <= 4 * kRmsVec * kThreads; }
+
+int rh_w8_merge_rmsnorm(const float* workspace, int ksplit, int T, int H, const float* scale, float* x,
+                        const float* norm_w, float eps, void* out, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(T > 0 && rh_w8_merge_rmsnorm_fits(H) && ksplit >= 1 && ksplit <= kMaxMergeSplit,
+             "w8_merge_rmsnorm: H must be a multiple of 4, at most 4096, and ksplit in 1..8");
+  RH_REQUIRE(workspace && scale && x && norm_w && out &&
+                 (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(norm_w) |
+                  reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+             "w8_merge_rmsnorm: x, norm_w and out must be 16-byte aligned");
+  RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_merge_rmsnorm_kernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                                   workspace, ksplit, T, H, scale, x, norm_w, eps, static_cast<half_t*>(out)));
   return 0;
 }
 

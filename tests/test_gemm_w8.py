@@ -218,3 +218,60 @@ def test_skinny_accumulates_and_limits(torch_mod, dev):
     assert "ksplit" in _lib.last_error()
     assert L.rh_gemm_w8_skinny(None, 256, None, None, None, 8, 256, 64, 0.0, 2, None, None) != 0
     assert "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("T,I,H,ks", [(17, 1024, 512, 2), (32, 5632, 2048, 3), (48, 2048, 4096, 8), (100, 1536, 576, 4)])
+def test_merge_fused_consumers_equal_the_chain(torch_mod, dev, T, I, H, ks):
+    """rh_gemm_w8_partials + rh_w8_merge_silu equals the split product + rh_silu_mul, and
+    rh_gemm_w8_partials + rh_w8_merge_rmsnorm equals the split product accumulated into the
+    residual (beta = 1) + rh_rmsnorm, byte for byte (same partials, same merge arithmetic)."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(T + I + H + ks)
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    split = (lambda *a: L.rh_gemm_w8_skinny(*a)) if T <= 64 else (lambda *a: L.rh_gemm_w8_split(*a))
+    print(f"fused merges: T={T} I={I} H={H} ksplit={ks}", flush=True)
+    # gate_up [2I, H] then SiLU
+    q, s, x = make(2 * I, H, T, seed=T + 1)
+    Wg, Sg, X = dt(q), dt(s), dt(x.view(np.int16))
+    ws = torch.empty(ks * T * 2 * I, device=dev)
+    gu = torch.empty((T, 2 * I), device=dev)
+    act_a = torch.empty((T, I), dtype=torch.int16, device=dev)
+    act_b = torch.empty((T, I), dtype=torch.int16, device=dev)
+    _lib.check(split(Wg.data_ptr(), H, Sg.data_ptr(), X.data_ptr(), gu.data_ptr(), T, H, 2 * I, 0.0, ks, ws.data_ptr(),
+                     None), "split product")
+    _lib.check(L.rh_silu_mul(gu.data_ptr(), T, I, act_a.data_ptr(), None), "rh_silu_mul")
+    _lib.check(L.rh_gemm_w8_partials(Wg.data_ptr(), H, X.data_ptr(), T, H, 2 * I, ks, ws.data_ptr(), None), "partials")
+    _lib.check(L.rh_w8_merge_silu(ws.data_ptr(), ks, T, I, Sg.data_ptr(), act_b.data_ptr(), None), "merge_silu")
+    torch.cuda.synchronize()
+    assert np.array_equal(act_a.cpu().numpy(), act_b.cpu().numpy())
+    # down [H, I] into the residual, then RMSNorm
+    q, s, a8 = make(H, I, T, seed=T + 2)
+    Wd, Sd, A = dt(q), dt(s), dt(a8.view(np.int16))
+    x0 = rng.standard_normal((T, H)).astype(np.float32)
+    nw = dt(rng.uniform(0.5, 1.5, H).astype(np.float32))
+    xa, xb = dt(x0), dt(x0)
+    ws2 = torch.empty(ks * T * H, device=dev)
+    na = torch.empty((T, H), dtype=torch.int16, device=dev)
+    nb = torch.empty((T, H), dtype=torch.int16, device=dev)
+    _lib.check(split(Wd.data_ptr(), I, Sd.data_ptr(), A.data_ptr(), xa.data_ptr(), T, I, H, 1.0, ks, ws2.data_ptr(),
+                     None), "split product (beta 1)")
+    _lib.check(L.rh_rmsnorm(xa.data_ptr(), None, T, nw.data_ptr(), H, 1e-5, na.data_ptr(), None), "rh_rmsnorm")
+    _lib.check(L.rh_gemm_w8_partials(Wd.data_ptr(), I, A.data_ptr(), T, I, H, ks, ws2.data_ptr(), None), "partials")
+    _lib.check(L.rh_w8_merge_rmsnorm(ws2.data_ptr(), ks, T, H, Sd.data_ptr(), xb.data_ptr(), nw.data_ptr(), 1e-5,
+                                     nb.data_ptr(), None), "merge_rmsnorm")
+    torch.cuda.synchronize()
+    assert np.array_equal(xa.cpu().numpy().view(np.uint32), xb.cpu().numpy().view(np.uint32))
+    assert np.array_equal(na.cpu().numpy(), nb.cpu().numpy())
+    check(xa.cpu().numpy() - x0, q, s, a8)  # and the product itself within the fp32 bound
+
+
+def test_merge_fused_limits(torch_mod, dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_w8_merge_rmsnorm_fits(4096) and not L.rh_w8_merge_rmsnorm_fits(4100) and not L.rh_w8_merge_rmsnorm_fits(8192)
+    assert L.rh_gemm_w8_partials(None, 128, None, 4, 128, 64, 1, None, None) != 0 and "ksplit" in _lib.last_error()
+    assert L.rh_w8_merge_silu(None, 2, 4, 12, None, None, None) != 0
