@@ -744,6 +744,16 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
                                      w8, ldw, scale, x, y, T, K, N, beta));
     return 0;
   }
+  if (T >= 5 && T <= 8 && N >= 14336) {
+    // 32 rows per workgroup: a quarter of the 8-row form's activation reads through L2
+    // (measured at T = 4 and 8 on Llama-3-8B's gate_up shape: L1 -> L2 read requests 1.5x
+    // those at T = 1, i.e. ~0.6x the weight bytes again in activations, with 16 rows).
+    // 4096 -> 14336 at T = 8 16.5 -> 15.4 us; at T = 4, or on matrices of 4096-14336 rows
+    // with K = 14336 (fewer than 448 workgroups), slower.
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 4>), dim3((N + 31) / 32), dim3(8 * kWave), 0,
+                                     s, w8, ldw, scale, x, y, T, K, N, beta));
+    return 0;
+  }
   if (T <= 8) {  // 16 rows per workgroup: half the activation reads of the 8-row form
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 2>), dim3((N + 15) / 16), dim3(8 * kWave), 0,
                                      s, w8, ldw, scale, x, y, T, K, N, beta));
