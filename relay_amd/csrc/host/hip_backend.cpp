@@ -23,6 +23,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <functional>
 #include <limits>
 #include <memory>
@@ -215,6 +216,7 @@ class HipBackend final : public Backend {
   static bool skinny(int K, int N, int T);
   void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
   static constexpr int kKvChunks = 16;                          // pieces of one KV transfer
+  static constexpr int kKvThreads = 4;                          // host threads copying them (8: no faster)
   static constexpr std::size_t kKvMinPiece = std::size_t(1) << 20;
   std::vector<hipEvent_t> kv_events_;                           // one per piece in flight
 
@@ -702,6 +704,44 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
   return static_cast<std::size_t>(R) * V;
 }
 
+// Runs share(j) for j = 0 .. workers - 1: share 0 on the calling thread, the others on
+// helper threads (a share whose thread cannot be started runs on the calling thread). Every
+// helper is joined before this returns, on every path; the first exception any share
+// threw is rethrown after the join.
+template <typename F>
+static void run_shares(int workers, F&& share) {
+  std::mutex mu;
+  std::exception_ptr err;
+  auto guarded = [&](int j) {
+    try {
+      share(j);
+    } catch (...) {
+      std::lock_guard<std::mutex> lock(mu);
+      if (!err) err = std::current_exception();
+    }
+  };
+  struct Joiner {
+    std::vector<std::thread> t;
+    ~Joiner() {
+      for (auto& x : t)
+        if (x.joinable()) x.join();
+    }
+  } helpers;
+  int started = 1;
+  for (int j = 1; j < workers; ++j) {
+    try {
+      helpers.t.emplace_back(guarded, j);
+      ++started;
+    } catch (const std::system_error&) {
+      break;
+    }
+  }
+  guarded(0);
+  for (int j = started; j < workers; ++j) guarded(j);
+  for (auto& t : helpers.t) t.join();
+  if (err) std::rethrow_exception(err);
+}
+
 void HipBackend::finish_forward(float* dst, std::size_t n) {
   if (!pending_) return;
   pending_ = false;
@@ -733,39 +773,13 @@ void HipBackend::finish_forward(float* dst, std::size_t n) {
   // allocated memory runs at ~10 GB/s: 25 MB of Llama-3 logits for 49 rows took ~2.5 ms).
   const auto* host = static_cast<const unsigned char*>(logits_host_.p);
   const int workers = bytes >= kLogitThreadBytes ? std::min(kLogitThreads, pieces) : 1;
-  std::atomic<bool> failed{false};
-  auto copy_share = [&](int j) {
+  run_shares(workers, [&](int j) {
     for (int i = j; i < pieces; i += workers) {
       const std::size_t a = i * piece, len = std::min(piece, bytes - a);
-      if (hipEventSynchronize(logit_events_[i]) != hipSuccess) {
-        failed = true;
-        return;
-      }
+      HIP_CHECK(hipEventSynchronize(logit_events_[i]));
       std::memcpy(reinterpret_cast<unsigned char*>(dst) + a, host + a, len);
     }
-  };
-  // Helper threads are joined by the guard on every path (a thread that cannot be started
-  // leaves its share to the calling thread), so no exception leaves a joinable thread behind.
-  struct Joiner {
-    std::vector<std::thread> t;
-    ~Joiner() {
-      for (auto& x : t)
-        if (x.joinable()) x.join();
-    }
-  } helpers;
-  int started = 1;
-  for (int j = 1; j < workers; ++j) {
-    try {
-      helpers.t.emplace_back(copy_share, j);
-      ++started;
-    } catch (const std::system_error&) {
-      break;
-    }
-  }
-  copy_share(0);
-  for (int j = started; j < workers; ++j) copy_share(j);
-  for (auto& t : helpers.t) t.join();
-  if (failed) throw std::runtime_error("HIP error while copying the logits");
+  });
 }
 
 // KV block traffic on the copy stream: gather into a contiguous device buffer and copy it
@@ -797,6 +811,9 @@ void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, v
   // Staging bytes [0, n bb) are K, [n bb, 2 n bb) V; piece i covers [i piece, (i+1) piece).
   const std::size_t piece = std::max<std::size_t>(kKvMinPiece, (bytes + kKvChunks - 1) / kKvChunks);
   const int pieces = static_cast<int>((bytes + piece - 1) / piece);
+  // The host-side copies between the caller's buffers and the pinned staging run on a few
+  // threads (one core moves ~10-25 GB/s; the DMA runs at the PCIe rate).
+  const int workers = bytes >= kLogitThreadBytes ? std::min(kKvThreads, pieces) : 1;
   auto user_copy = [&](std::size_t a, std::size_t len, bool to_user) {
     // [a, a + len) of the staging buffer to / from k_out|k_in and v_out|v_in.
     while (len) {
@@ -818,16 +835,22 @@ void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, v
       HIP_CHECK(hipMemcpyAsync(host + a, kv_stage_dev_.p + a, len, hipMemcpyDeviceToHost, copy_stream_));
       HIP_CHECK(hipEventRecord(kv_events_[i], copy_stream_));
     }
-    for (int i = 0; i < pieces; ++i) {
-      HIP_CHECK(hipEventSynchronize(kv_events_[i]));
-      user_copy(i * piece, std::min(piece, bytes - i * piece), true);
-    }
+    run_shares(workers, [&](int j) {
+      for (int i = j; i < pieces; i += workers) {
+        HIP_CHECK(hipEventSynchronize(kv_events_[i]));
+        user_copy(i * piece, std::min(piece, bytes - i * piece), true);
+      }
+    });
   } else {
-    for (int i = 0; i < pieces; ++i) {
-      const std::size_t a = i * piece, len = std::min(piece, bytes - a);
-      user_copy(a, len, false);
-      HIP_CHECK(hipMemcpyAsync(kv_stage_dev_.p + a, host + a, len, hipMemcpyHostToDevice, copy_stream_));
-    }
+    // Each share copies its pieces into the staging buffer and queues their uploads (the
+    // scatter below runs after every share's uploads are queued).
+    run_shares(workers, [&](int j) {
+      for (int i = j; i < pieces; i += workers) {
+        const std::size_t a = i * piece, len = std::min(piece, bytes - a);
+        user_copy(a, len, false);
+        HIP_CHECK(hipMemcpyAsync(kv_stage_dev_.p + a, host + a, len, hipMemcpyHostToDevice, copy_stream_));
+      }
+    });
     RH_CHECK(rh_kv_scatter(kc_.p + off, vc_.p + off, kv_ids_dev_.p, static_cast<int>(n), bb, kv_stage_dev_.p,
                            copy_stream_));
     HIP_CHECK(hipStreamSynchronize(copy_stream_));
