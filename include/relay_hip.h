@@ -256,12 +256,20 @@ int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, const void* x,
  * narrow matrices fill the GPU: each range writes its raw sums to workspace (fp32,
  * ksplit * T * N values, N a multiple of 4) and a second launch adds them in range order
  * before the scale and beta (deterministic, independent of timing). Calls sharing a
- * workspace must not overlap. rh_gemm_w8_plan(T, K, N) gives the split measured best for
- * the shape (-1 if K is not a positive multiple of 64). No counterpart in relay, which
- * dequantizes the whole matrix and calls cublasGemmEx (cuda_backend.cu:718-722). */
+ * workspace must not overlap. rh_gemm_w8_plan(T, K, N) gives the split of the plan for the
+ * shape (-1 if K is not a positive multiple of 64): above 64 tokens with K a multiple of
+ * 128, the minimum of a timing model fitted to measurements over the kernels (128 x 128 and
+ * 128 x 96 tiles on 128-k steps, 256 x 96 on 64-k steps) and 1-8 ranges; otherwise the
+ * 128 x 128 or 256 x 96 tile on 64-k steps. rh_gemm_w8_kernel(T, K, N, ksplit) names the
+ * kernel rh_gemm_w8_split runs for that split (0: 128 x 128 on 64-k steps, 1: 256 x 96,
+ * 2: 128 x 128 on 128-k steps, 3: 128 x 96 on 128-k steps; -1 for bad arguments); the
+ * kernels differ in the order in which each MFMA adds up its 16 k. No counterpart in
+ * relay, which dequantizes the whole matrix and calls cublasGemmEx
+ * (cuda_backend.cu:718-722). */
 int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K,
                      int N, float beta, int ksplit, float* workspace, void* stream);
 int rh_gemm_w8_plan(int T, int K, int N);
+int rh_gemm_w8_kernel(int T, int K, int N, int ksplit);
 
 /* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 32-token tile (64 tokens above 32) and K cut
  * into ksplit ranges (1 <= ksplit <= 8, at most K / 64), so that decode batches of 17-64
@@ -273,8 +281,8 @@ int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const v
 
 /* The first half of a split int8 product, for consumers that merge it themselves: the raw
  * sums of ksplit K ranges (2 <= ksplit <= 8, at most K / 64) into workspace [ksplit][T][N]
- * (N a multiple of 4), with the tile rh_gemm_w8_skinny (T <= 64) or rh_gemm_w8_split takes
- * at this T; no scale is applied. The merges below then add the ranges in order and apply
+ * (N a multiple of 4), with the kernel rh_gemm_w8_skinny (T <= 64) or rh_gemm_w8_split
+ * (rh_gemm_w8_kernel) runs for this T and split; no scale is applied. The merges below then add the ranges in order and apply
  * the scale, with the arithmetic of the two-launch chain (same bits). */
 int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N, int ksplit,
                         float* workspace, void* stream);

@@ -86,6 +86,52 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w8_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 }
 
+// The tile's results: register 4 q + r of block (a, b) in lane (c, h) is row 32 (AN w + a) +
+// 8 q + 4 h + r, token 32 b + c. ksn > 1: this K range's raw sums go to the workspace (the
+// host requires N % 4 == 0 there) and w8_split_merge_kernel (or a consumer) adds the ranges
+// in order. (A merge by the last workgroup of each tile to arrive, through coherent stores
+// and loads and an arrival counter, measured 1.4-6x slower than the merge launch at T =
+// 32-560: the partials are written through.)
+template <int AN, int BT>
+__device__ __forceinline__ void w8_write_out(const float16v (&acc)[AN][BT], int w, int c, int h, int n0, int t0, int kz,
+                                             int T, int N, int ksn, float* ws, const float* __restrict__ scale, float* y,
+                                             float beta, int vec_out) {
+  auto store = [&](float4v v, int t, int n) {
+    if (vec_out && n + 3 < N) {
+      const float4v sc = {scale[n], scale[n + 1], scale[n + 2], scale[n + 3]};
+      float* yp = y + static_cast<int64_t>(t) * N + n;
+      v = v * sc;
+      if (beta != 0.0f) v += beta * *reinterpret_cast<const float4v*>(yp);
+      *reinterpret_cast<float4v*>(yp) = v;
+    } else {
+      float* yp = y + static_cast<int64_t>(t) * N;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < N) {
+          const float o = v[r] * scale[n + r];
+          yp[n + r] = o + (beta != 0.0f ? beta * yp[n + r] : 0.0f);
+        }
+    }
+  };
+#pragma unroll
+  for (int b = 0; b < BT; ++b) {
+    const int t = t0 + 32 * b + c;
+    if (t >= T) continue;
+#pragma unroll
+    for (int a = 0; a < AN; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 32 * (AN * w + a) + 8 * q + 4 * h;
+        if (n >= N) continue;
+        const float4v v = {acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]};
+        if (ksn > 1)
+          *reinterpret_cast<float4v*>(ws + (static_cast<int64_t>(kz) * T + t) * N + n) = v;
+        else
+          store(v, t, n);
+      }
+  }
+}
+
 template <int AN, int BT, int WPE>
 __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                            const float* __restrict__ scale,
@@ -189,77 +235,205 @@ __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restr
   }
   if (s < nsteps) compute(wa, 0);
 
-  // Register 4 q + r of block (a, b) in lane (c, h): row 32 (AN w + a) + 8 q + 4 h + r,
-  // token 32 b + c.
-  auto store = [&](float4v v, int t, int n) {
-    if (vec_out && n + 3 < N) {
-      const float4v sc = {scale[n], scale[n + 1], scale[n + 2], scale[n + 3]};
-      float* yp = y + static_cast<int64_t>(t) * N + n;
-      v = v * sc;
-      if (beta != 0.0f) v += beta * *reinterpret_cast<const float4v*>(yp);
-      *reinterpret_cast<float4v*>(yp) = v;
-    } else {
-      float* yp = y + static_cast<int64_t>(t) * N;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (n + r < N) {
-          const float o = v[r] * scale[n + r];
-          yp[n + r] = o + (beta != 0.0f ? beta * yp[n + r] : 0.0f);
-        }
-    }
-  };
-  // ksn > 1: this K range's raw sums to the workspace (the host requires N % 4 == 0 there);
-  // w8_split_merge_kernel adds the ranges in order. (A merge by the last workgroup of each
-  // tile to arrive, through coherent stores and loads and an arrival counter, measured
-  // 1.4-6x slower than the merge launch at T = 32-560: the partials are written through.)
-  if (ksn > 1) {
-#pragma unroll
-    for (int b = 0; b < BT; ++b) {
-      const int t = t0 + 32 * b + c;
-      if (t >= T) continue;
-#pragma unroll
-      for (int a = 0; a < AN; ++a)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = n0 + 32 * (AN * w + a) + 8 * q + 4 * h;
-          if (n >= N) continue;
-          *reinterpret_cast<float4v*>(ws + (static_cast<int64_t>(kz) * T + t) * N + n) =
-              float4v{acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]};
-        }
-    }
-    return;
-  }
-#pragma unroll
-  for (int b = 0; b < BT; ++b) {
-    const int t = t0 + 32 * b + c;
-    if (t >= T) continue;
-#pragma unroll
-    for (int a = 0; a < AN; ++a)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + 32 * (AN * w + a) + 8 * q + 4 * h;
-        if (n >= N) continue;
-        store(float4v{acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]}, t, n);
-      }
-  }
+  w8_write_out<AN, BT>(acc, w, c, h, n0, t0, kz, T, N, ksn, ws, scale, y, beta, vec_out);
 }
 
-// Tiles: 128 rows x 128 tokens (3 waves per SIMD fit), or 256 x 96 (2 per SIMD) when the
-// grid already has >= 768 of the smaller tiles (28672 x 4096 at T = 560: 183 -> 167 us).
-struct W8TilePlan {
-  bool big;
+// ---- the wide-step kernel ---------------------------------------------------------------
+//
+// 128 rows x 32 BT tokens, 4 waves (wave w: rows 32 w .. +32, all tokens), two workgroups per
+// CU. Per 128-k step lane (c, h) reads the 64 contiguous bytes W8[row c, k0 + 64 h .. +64)
+// (four 16-byte loads), and k-slice j (j = 0..7) takes slots 8 h .. 8 h + 7 from k0 + 64 h +
+// 8 j on both operands, so every lane's bytes of a step are one half of a 128-byte line.
+// W runs two steps ahead in two register sets, x two steps ahead in two register sets
+// staged into a double-buffered LDS tile. Steps come in pairs with no branch inside; a
+// step past the range (the second of an odd count) computes with a zero x tile, so its
+// products add exact zeros. Measured against the 64-k tile kernel (us, in isolation; the
+// kernel / its best K split at each point): Llama-3-8B at T = 560: 6144 x 4096 45.6 / 56.9,
+// 4096 x 4096 37.8 (96-token tile) / 44.4, 4096 x 14336 100.2 / 107.3; at T = 512:
+// TinyLlama 2560 x 2048 20.9 / 29.8, 11264 x 2048 42.2 / 58.7, 2048 x 5632 30.1 / 35.7.
+template <int BT>
+__global__ __launch_bounds__(256, 2) void w8_wide_kernel(const int8_t* __restrict__ w8, int64_t ldw,
+                                                         const float* __restrict__ scale, const half_t* __restrict__ x,
+                                                         float* y, int T, int K, int N, float beta, float* ws,
+                                                         int n_row, int n_tok, int ksn, int vec_out) {
+  constexpr int KS = 128, XR = KS + 8, TB = 32 * BT, NX = 2 * BT;  // NX 16-byte x pieces per thread
+  __shared__ __attribute__((aligned(16))) half_t xs[2][TB * XR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int total = n_row * n_tok * ksn, L = blockIdx.x;
+  const int per = total / 8, rem = total % 8, xcd = L % 8;
+  const int idx = xcd * per + min(xcd, rem) + L / 8;
+  const int tok = idx % n_tok, rk = idx / n_tok, kz = rk % ksn, row = rk / ksn;
+  const int n0 = row * 128, t0 = tok * TB;
+  const int nall = K / KS, sbeg = kz * nall / ksn, nsteps = (kz + 1) * nall / ksn - sbeg;
+
+  const __amdgpu_buffer_rsrc_t wrs = w8_rsrc(w8 + static_cast<int64_t>(n0) * ldw + static_cast<int64_t>(sbeg) * KS);
+  const __amdgpu_buffer_rsrc_t xrs = w8_rsrc(x + static_cast<int64_t>(sbeg) * KS);
+  const int woff = (min(n0 + 32 * w + c, N - 1) - n0) * static_cast<int>(ldw) + 64 * h;
+  int xoff[NX], xst[NX];  // piece j: token e / 16, k piece e % 16, e = tid + 256 j
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int e = tid + 256 * j, r = e / 16, col = e % 16;
+    xoff[j] = (min(t0 + r, T - 1) * K + 8 * col) * 2;
+    xst[j] = r * XR + 8 * col;
+  }
+  uint4v wr[2][4], xr[2][NX];
+  auto load_w = [&](int u, int s) {
+    const int so = min(s, nsteps - 1) * KS;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) wr[u][v] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff + 16 * v, so, 0);
+  };
+  auto load_x = [&](int u, int s) {
+    const int so = min(s, nsteps - 1) * KS * 2;
+#pragma unroll
+    for (int j = 0; j < NX; ++j) xr[u][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[j], so, 0);
+  };
+  auto stage = [&](int u, bool live) {
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      uint4v v = xr[u][j];
+      if (!live) v = uint4v{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4v*>(&xs[u][xst[j]]) = v;
+    }
+  };
+  float16v acc[1][BT];
+#pragma unroll
+  for (int b = 0; b < BT; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[0][b][i] = 0.0f;
+
+  auto compute = [&](int u) {
+    const half_t* xb = &xs[u][c * XR + 64 * h];
+    half8 bq[2][BT], av[2];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) bq[0][b] = *reinterpret_cast<const half8*>(xb + 32 * b * XR);
+    av[0] = int8x8_to_half8_w8(wr[u][0][0], wr[u][0][1]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int cu = j & 1, nx = cu ^ 1;
+      if (j < 7) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) bq[nx][b] = *reinterpret_cast<const half8*>(xb + 32 * b * XR + 8 * (j + 1));
+        av[nx] = int8x8_to_half8_w8(wr[u][(j + 1) >> 1][2 * ((j + 1) & 1)], wr[u][(j + 1) >> 1][2 * ((j + 1) & 1) + 1]);
+      }
+#pragma unroll
+      for (int b = 0; b < BT; ++b) acc[0][b] = mfma32x32x16(av[cu], bq[cu][b], acc[0][b]);
+    }
+  };
+  // Step s: issue x(s + 2) into x set s & 1 (staged already), compute s from LDS buffer
+  // s & 1, issue W(s + 2) into W set s & 1, stage x(s + 1) into LDS buffer (s + 1) & 1.
+  load_w(0, 0);
+  load_x(0, 0);
+  load_w(1, 1);
+  load_x(1, 1);
+  stage(0, true);
+  __syncthreads();
+  for (int s = 0; s < nsteps; s += 2) {
+    load_x(0, s + 2);
+    compute(0);
+    load_w(0, s + 2);
+    stage(1, s + 1 < nsteps);
+    __syncthreads();
+    load_x(1, s + 3);
+    compute(1);
+    load_w(1, s + 3);
+    stage(0, s + 2 < nsteps);
+    __syncthreads();
+  }
+  w8_write_out<1, BT>(acc, w, c, h, n0, t0, kz, T, N, ksn, ws, scale, y, beta, vec_out);
+}
+
+template <int BT>
+int launch_w8_wide(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K, int N,
+                   float beta, hipStream_t s, int ksplit, float* ws) {
+  // ksplit < 0: -ksplit ranges, partials only (no merge launch; a fused consumer merges).
+  const bool merge = ksplit > 0;
+  ksplit = merge ? ksplit : -ksplit;
+  const int n_row = (N + 127) / 128, n_tok = (T + 32 * BT - 1) / (32 * BT);
+  const int64_t total = static_cast<int64_t>(n_row) * n_tok * ksplit;
+  RH_REQUIRE(total < (int64_t(1) << 31), "gemm_w8: grid too large");
+  const int vec_out = N % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((w8_wide_kernel<BT>), dim3(static_cast<unsigned>(total)), dim3(256), 0, s, w8, ldw,
+                                   scale, x, y, T, K, N, beta, ws, n_row, n_tok, ksplit, vec_out));
+  if (ksplit > 1 && merge) {
+    const int64_t quads = static_cast<int64_t>(T) * N / 4;
+    RH_TRY_LAUNCH(hipLaunchKernelGGL(w8_split_merge_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                                     s, ws, ksplit, T, N, scale, y, beta));
+  }
+  return 0;
+}
+
+// Kernels and K splits above 64 tokens. kTile128 (w8_tile_kernel<1, 4, 3>) and kTileBig
+// (<2, 3, 2>, 256 x 96) take any K that is a multiple of 64; the wide-step kernels
+// (128 x 128 and 128 x 96 tiles) need K a multiple of 128 and at least one 128-k step per
+// range.
+enum W8Cfg { kTile128 = 0, kTileBig = 1, kWide128 = 2, kWide96 = 3 };
+struct W8Plan {
+  int cfg;
   int ksplit;
 };
 
-W8TilePlan w8_tile_plan(int T, int K, int N) {
+// The previous plan, kept for K not a multiple of 128: the 128 x 128 tile with K ranges
+// until the grid has >= 480 workgroups (at most 8 ranges of >= 4 steps), or the 256 x 96
+// tile when there are >= 768 of the smaller tiles.
+W8Plan w8_tile_plan(int T, int K, int N) {
   const int small = ((N + 127) / 128) * ((T + 127) / 128);
-  if (small >= 768) return {true, 1};
-  // K ranges until the grid has >= 480 workgroups (about two per CU), at most 8 and each
-  // at least 4 steps of 64 k (measured at Llama-3-8B and TinyLlama shapes, T = 128-560).
+  if (small >= 768) return {kTileBig, 1};
   int ks = small >= 384 ? 1 : std::min(8, (480 + small - 1) / small);
   while (ks > 1 && (K / 64) / ks < 4) --ks;
   if (N % 4) ks = 1;
-  return {false, ks};
+  return {kTile128, ks};
+}
+
+// A timing model of one product, in microseconds, fitted to 464 measured (kernel, split)
+// points over eight Llama-3-8B and TinyLlama matrices at T = 128-560 (log-RMS error 8.6%).
+// A workgroup's time is (128-k steps in its range + 1.83) x a per-tile factor (the
+// 128 x 96 tile 0.85, 256 x 96 1.34 of the 128 x 128 one), nearly independent of how many
+// tokens its tile holds; the grid runs as rounds of 256 workgroups (two share a CU, at the
+// same total rate; one alone runs at 0.95 / 0.88 / 0.70 of it); a split adds its merge,
+// 2.16 us + 1.53 us per million partial sums read and written. Choosing the minimum of the
+// model picks a kernel within 1.3% of the measured best on average over those points
+// (worst 11%), against 22% above it for the previous plan.
+double w8_model_us(int cfg, int T, int K, int N, int ks) {
+  const int rows = cfg == kTileBig ? 256 : 128, toks = cfg == kWide128 ? 128 : 96;
+  const double factor = cfg == kWide128 ? 1.0 : cfg == kWide96 ? 0.8513 : 1.34;
+  const double alone = cfg == kWide128 ? 0.8826 : cfg == kWide96 ? 0.9462 : 0.7039;
+  const int64_t wgs = static_cast<int64_t>((N + rows - 1) / rows) * ((T + toks - 1) / toks) * ks;
+  const double w = (K / 128.0 / ks + 1.8343) * factor;
+  const int64_t rounds = (wgs + 255) / 256;
+  double t = static_cast<double>(rounds / 2) * 2.0 * w + static_cast<double>(rounds % 2) * w / alone;
+  if (ks > 1) t += 2.1571 + 1.5261e-6 * (ks + 1) * static_cast<double>(T) * N;
+  return t;
+}
+
+bool w8_wide_fits(int K, int ks) { return K % 128 == 0 && ks <= K / 128; }
+
+// The kernel for a given split: the model's choice among the kernels that take it.
+int w8_cfg_for(int T, int K, int N, int ks) {
+  if (T <= 64 || !w8_wide_fits(K, ks)) return ks == 1 && w8_tile_plan(T, K, N).cfg == kTileBig ? kTileBig : kTile128;
+  int best = kWide128;
+  double tb = w8_model_us(kWide128, T, K, N, ks);
+  for (int cfg : {kWide96, kTileBig}) {
+    if (cfg == kTileBig && ks != 1) continue;
+    const double t = w8_model_us(cfg, T, K, N, ks);
+    if (t < tb) tb = t, best = cfg;
+  }
+  return best;
+}
+
+// Kernel and split: the model's minimum over the wide-step kernels at 1-8 ranges of >= 2
+// steps and the 256 x 96 tile unsplit.
+W8Plan w8_plan(int T, int K, int N) {
+  if (T <= 64 || K % 128) return w8_tile_plan(T, K, N);
+  W8Plan best = {kTileBig, 1};
+  double tb = w8_model_us(kTileBig, T, K, N, 1);
+  for (int ks = 1; ks <= kMaxW8Split && (K / 128) / ks >= 2; ++ks) {
+    if (ks > 1 && N % 4) break;
+    for (int cfg : {kWide128, kWide96}) {
+      const double t = w8_model_us(cfg, T, K, N, ks);
+      if (t < tb) tb = t, best = {cfg, ks};
+    }
+  }
+  return best;
 }
 
 template <int AN, int BT, int WPE>
@@ -280,6 +454,16 @@ int launch_w8_tile(const int8_t* w8, int64_t ldw, const float* scale, const half
                                      s, ws, ksplit, T, N, scale, y, beta));
   }
   return 0;
+}
+
+int launch_w8_cfg(int cfg, const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K,
+                  int N, float beta, hipStream_t s, int ksplit, float* ws) {
+  switch (cfg) {
+    case kTileBig: return launch_w8_tile<2, 3, 2>(w8, ldw, scale, x, y, T, K, N, beta, s, ksplit, ws);
+    case kWide128: return launch_w8_wide<4>(w8, ldw, scale, x, y, T, K, N, beta, s, ksplit, ws);
+    case kWide96: return launch_w8_wide<3>(w8, ldw, scale, x, y, T, K, N, beta, s, ksplit, ws);
+    default: return launch_w8_tile<1, 4, 3>(w8, ldw, scale, x, y, T, K, N, beta, s, ksplit, ws);
+  }
 }
 
 }  // namespace
@@ -304,13 +488,17 @@ extern "C" int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, con
   if (int rc = gemm_w8_checks(w8, ldw, x, T, K, N)) return rc;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
-  if (w8_tile_plan(T, K, N).big) return launch_w8_tile<2, 3, 2>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
-  return launch_w8_tile<1, 4, 3>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
+  return launch_w8_cfg(w8_cfg_for(T, K, N, 1), w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
 }
 
 extern "C" int rh_gemm_w8_plan(int T, int K, int N) {
   if (T < 1 || K <= 0 || K % 64 || N <= 0) return -1;
-  return w8_tile_plan(T, K, N).ksplit;
+  return w8_plan(T, K, N).ksplit;
+}
+
+extern "C" int rh_gemm_w8_kernel(int T, int K, int N, int ksplit) {
+  if (T < 1 || K <= 0 || K % 64 || N <= 0 || ksplit < 1 || ksplit > kMaxW8Split || ksplit > K / 64) return -1;
+  return w8_cfg_for(T, K, N, ksplit);
 }
 
 extern "C" int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T,
@@ -323,9 +511,7 @@ extern "C" int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scal
   RH_REQUIRE(ksplit == 1 || N % 4 == 0, "gemm_w8_split: ksplit > 1 needs N a multiple of 4");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
-  if (ksplit == 1 && w8_tile_plan(T, K, N).big)
-    return launch_w8_tile<2, 3, 2>(w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
-  return launch_w8_tile<1, 4, 3>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
+  return launch_w8_cfg(w8_cfg_for(T, K, N, ksplit), w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
 }
 
 extern "C" int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N, int ksplit,
@@ -340,7 +526,7 @@ extern "C" int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x,
   // point takes for this T.
   if (T <= 32) return launch_w8_tile<1, 1, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
   if (T <= 64) return launch_w8_tile<1, 2, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
-  return launch_w8_tile<1, 4, 3>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
+  return launch_w8_cfg(w8_cfg_for(T, K, N, ksplit), w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
 }
 
 // 17-64 tokens: 128 rows x 32 tokens (x 64 above 32 tokens), four waves per SIMD, K cut

@@ -92,6 +92,9 @@ def test_llama3_shapes_at_the_mixed_batch(torch_mod, dev, N, K):
 def test_wide_matrix_at_the_mixed_batch(torch_mod, dev):
     """Llama-3-8B's gate_up (28672 x 4096) at T = 560 runs the 256 x 96 tile; 1536 rows
     spread over the matrix are checked against float64."""
+    from relay_amd import _lib
+
+    assert _lib.lib().rh_gemm_w8_kernel(560, 4096, 28672, 1) == 1
     q, s, x = make(28672, 4096, 560, seed=7)
     rows = np.sort(np.random.default_rng(8).choice(28672, 1536, replace=False))
     check(run(torch_mod, dev, q, s, x), q, s, x, rows=rows)
@@ -118,10 +121,43 @@ def test_plan(dev):
 
     L = _lib.lib()
     # Llama-3-8B at config 5's 560 tokens: qkv, wo, gate_up, down
-    assert [L.rh_gemm_w8_plan(560, k, n) for n, k in ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))] == \
-        [2, 3, 1, 3]
+    shapes = ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))
+    assert [L.rh_gemm_w8_plan(560, k, n) for n, k in shapes] == [1, 1, 1, 3]
+    assert [L.rh_gemm_w8_kernel(560, k, n, L.rh_gemm_w8_plan(560, k, n)) for n, k in shapes] == [2, 3, 1, 2]
+    # TinyLlama at 512-token prefill chunks: qkv, wo, gate_up, down
+    shapes = ((2560, 2048), (2048, 2048), (11264, 2048), (2048, 5632))
+    assert [L.rh_gemm_w8_plan(512, k, n) for n, k in shapes] == [1, 2, 1, 4]
     assert L.rh_gemm_w8_plan(560, 100, 64) == -1 and L.rh_gemm_w8_plan(0, 64, 64) == -1
-    assert 1 <= L.rh_gemm_w8_plan(100, 128, 4096) <= 2  # ranges of at least 4 steps of 64 k
+    assert L.rh_gemm_w8_plan(100, 128, 4096) == 1  # ranges of at least two 128-k steps
+    # K not a multiple of 128: the 64-k step kernels; at most 64 tokens: the 128 x 128 tile
+    assert L.rh_gemm_w8_kernel(300, 576, 1536, 1) == 0 and L.rh_gemm_w8_kernel(64, 4096, 4096, 2) == 0
+    assert L.rh_gemm_w8_kernel(300, 1024, 1024, 9) == -1 and L.rh_gemm_w8_kernel(300, 1024, 1024, 8) in (2, 3)
+
+
+WIDE_CASES = [(65, 256, 4096, 4), (97, 1000, 1280, 3), (200, 250, 640, 1), (300, 512, 128, 1), (450, 132, 1152, 5),
+              (560, 2048, 2048, 2), (128, 4096, 640, 5), (250, 4096, 1280, 3), (512, 2048, 1152, 3)]
+
+
+@pytest.mark.parametrize("T,N,K,ks", WIDE_CASES)
+def test_wide_step_kernels(torch_mod, dev, T, N, K, ks):
+    """The 128-k step kernels (128 x 128 and 128 x 96 tiles): odd step counts per range (the
+    paired loop's zero step), one step, partial row and token tiles, N not a multiple of 4
+    (scalar stores), several K ranges; within the fp32 bound and the same bits on a repeat."""
+    from relay_amd import _lib
+
+    cfg = _lib.lib().rh_gemm_w8_kernel(T, K, N, ks)
+    assert cfg in (2, 3), cfg
+    q, s, x = make(N, K, T, seed=T * 7 + N + K + ks)
+    y = run_split(torch_mod, dev, q, s, x, ks)
+    check(y, q, s, x)
+    assert np.array_equal(y.view(np.uint32), run_split(torch_mod, dev, q, s, x, ks).view(np.uint32))
+
+
+def test_wide_step_kernels_cover_both_tiles(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert {L.rh_gemm_w8_kernel(T, K, N, ks) for T, N, K, ks in WIDE_CASES} == {2, 3}
 
 
 def test_beta_accumulates(torch_mod, dev):
@@ -220,7 +256,8 @@ def test_skinny_accumulates_and_limits(torch_mod, dev):
     assert "workspace" in _lib.last_error()
 
 
-@pytest.mark.parametrize("T,I,H,ks", [(17, 1024, 512, 2), (32, 5632, 2048, 3), (48, 2048, 4096, 8), (100, 1536, 576, 4)])
+@pytest.mark.parametrize("T,I,H,ks", [(17, 1024, 512, 2), (32, 5632, 2048, 3), (48, 2048, 4096, 8), (100, 1536, 576, 4),
+                                      (200, 1024, 1024, 3)])
 def test_merge_fused_consumers_equal_the_chain(torch_mod, dev, T, I, H, ks):
     """rh_gemm_w8_partials + rh_w8_merge_silu equals the split product + rh_silu_mul, and
     rh_gemm_w8_partials + rh_w8_merge_rmsnorm equals the split product accumulated into the
