@@ -213,27 +213,55 @@ __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restr
     }
   };
   // Step s issues x(s + 1), computes s, then issues W(s + 2) into the set s just used.
-  // The loop has one back edge and no exit in its body (an exit there made the compiler
-  // keep two copies of the accumulators); an odd last step runs after it.
-  load_x(0);
-  load_w(wa, 0);
-  load_w(wb, 1);
-  stage(0);
-  __syncthreads();
-  int s = 0;
-  for (; s + 1 < nsteps; s += 2) {
-    load_x(s + 1);
-    compute(wa, 0);
-    load_w(wa, s + 2);
-    stage(1);
-    __syncthreads();
-    load_x(s + 2);
-    compute(wb, 1);
-    load_w(wb, s + 3);
+  if constexpr (AN * BT == 2 || AN * BT == 4) {
+    // The 128 x 64 and 128 x 128 tiles: one back edge and no exit in the loop body (an exit
+    // there made the compiler keep two copies of the accumulators); an odd last step runs
+    // after it.
+    load_x(0);
+    load_w(wa, 0);
+    load_w(wb, 1);
     stage(0);
     __syncthreads();
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+      load_x(s + 1);
+      compute(wa, 0);
+      load_w(wa, s + 2);
+      stage(1);
+      __syncthreads();
+      load_x(s + 2);
+      compute(wb, 1);
+      load_w(wb, s + 3);
+      stage(0);
+      __syncthreads();
+    }
+    if (s < nsteps) compute(wa, 0);
+  } else {
+    // The 128 x 32 and 256 x 96 tiles: pairs of steps, the second under a (uniform) test.
+    // Measured against the form above, same process (us): 256 x 96 at 28672 x 4096, T = 560
+    // 168.5 -> 160.7; 128 x 32 at T = 32, 4096 x 14336 in 8 ranges 24.8 -> 21.8, 2048 x 5632
+    // in 8 ranges 12.3 -> 11.7, 11264 x 2048 in 2 ranges 15.2 -> 13.6. (On the 128 x 64 tile
+    // this form was slower: 40.6 -> 51.2 at 4096 x 14336, T = 32, 4 ranges.)
+    load_w(wa, 0);
+    load_w(wb, 1);
+    load_x(0);
+    stage(0);
+    __syncthreads();
+    for (int s = 0; s < nsteps; s += 2) {
+      load_x(s + 1);
+      compute(wa, 0);
+      load_w(wa, s + 2);
+      stage(1);
+      __syncthreads();
+      if (s + 1 < nsteps) {
+        load_x(s + 2);
+        compute(wb, 1);
+        load_w(wb, s + 3);
+        stage(0);
+      }
+      __syncthreads();
+    }
   }
-  if (s < nsteps) compute(wa, 0);
 
   w8_write_out<AN, BT>(acc, w, c, h, n0, t0, kz, T, N, ksn, ws, scale, y, beta, vec_out);
 }
