@@ -412,8 +412,9 @@ W8Plan w8_tile_plan(int T, int K, int N) {
   return {kTile128, ks};
 }
 
-// A timing model of one product, in microseconds, fitted to 464 measured (kernel, split)
-// points over eight Llama-3-8B and TinyLlama matrices at T = 128-560 (log-RMS error 8.6%).
+// A timing model of one product, in microseconds, fitted to 1088 measured (kernel, split)
+// pairs over eight Llama-3-8B and TinyLlama matrices at eight T from 128 to 560 (log-RMS
+// error 5.6%).
 // A workgroup's time is (128-k steps in its range + 1.83) x a per-tile factor (the
 // 128 x 96 tile 0.85, 256 x 96 1.34 of the 128 x 128 one), nearly independent of how many
 // tokens its tile holds; the grid runs as rounds of 256 workgroups (two share a CU, at the
