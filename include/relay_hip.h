@@ -186,6 +186,14 @@ int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, i
                              const int* tables, void* kpool, void* vpool, void* q_out, float q_scale, int heads,
                              int kv_heads, int head_dim, int block_size, void* stream);
 
+/* act[t, a] = fp16(silu(g) * u), g and u the rows a and I + a of rh_gemv_int8's product of
+ * the fused gate/up matrix W8 [2 I, K] (scale [2 I]) with x fp16 [T, K], for 1 <= T <= 8;
+ * act fp16 [T, I]. The same bits as rh_gemv_int8 into an fp32 [T, 2 I] buffer followed by
+ * rh_silu_mul, in one launch (each workgroup holds both halves of its outputs). No
+ * counterpart in relay (gemm then silu_mul_kernel, cuda_backend.cu:590-591). */
+int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
+                              void* act, int T, int K, int I, void* stream);
+
 /* y[t, n] = sum_k W16[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for 1 <= T <= 32:
  * the dense projection at decode batch sizes. W16 fp16 [N, K] rows ldw elements apart
  * (ldw >= K, a multiple of 8); x fp16 [T, K]; y fp32 [T, N]; K a multiple of 16; W16 and x

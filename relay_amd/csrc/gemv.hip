@@ -627,7 +627,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_kernel(const half_t* _
 // of matching products: lane (j = 2t + h, g) keeps rows 2g and 2g + 1 of half h for token t,
 // a lane shuffle adds the other half, and LDS sums the WAVES waves (which split K in runs of
 // 128) in a fixed order. DEPTH steps are loaded before any is used.
-template <int WAVES, int DEPTH, bool F16_SCALE, int RT = 1>
+//
+// SILU: W is the fused [gate; up] matrix of N = 2 I rows and the workgroup's 8 RT rows are
+// gate rows a0 .. a0 + 3 and up rows I + a0 .. I + a0 + 3 of each 8-row group (a0 = 4 RT
+// blockIdx.x + 4 rt), so one workgroup holds both halves of 4 RT outputs and writes act[t, a]
+// = fp16(silu(g) * u) (fp16 [T, I]) instead of y: the values of this kernel's plain form
+// followed by silu_mul_vec_kernel, bit for bit (same sums in the same order, same
+// epilogue arithmetic), one launch fewer.
+template <int WAVES, int DEPTH, bool F16_SCALE, int RT = 1, bool SILU = false>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                                      const void* __restrict__ scale,
                                                                      const half_t* __restrict__ x, float* y, int T,
@@ -638,21 +645,30 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
   const int c = lane & 15, g = lane >> 4;
   const int r = c >> 1, h = c & 1;  // A row: W row r0 + 8 rt + r, half h; B column: token r, half h
   const int r0 = blockIdx.x * 8 * RT;
+  const int I = N / 2, a0 = blockIdx.x * 4 * RT;  // SILU only
   const int nsteps = (K + 127) / 128;
   const int per = (nsteps + WAVES - 1) / WAVES;
   const int s0 = w * per, s1 = min(nsteps, s0 + per);
   // Thread 8 RT t + i writes y[t, r0 + i]; its scale and old y are loaded before the weights.
-  const int wt = threadIdx.x / (8 * RT), wn = r0 + static_cast<int>(threadIdx.x % (8 * RT));
-  const bool writer = static_cast<int>(threadIdx.x) < 8 * RT * T && wn < N;
-  float sc = 0.0f, yold = 0.0f;
+  // (SILU: thread 4 RT t + j writes act[t, a0 + j].)
+  const int wt = threadIdx.x / ((SILU ? 4 : 8) * RT), wj = static_cast<int>(threadIdx.x % ((SILU ? 4 : 8) * RT));
+  const int wn = SILU ? a0 + wj : r0 + wj;
+  const bool writer = static_cast<int>(threadIdx.x) < (SILU ? 4 : 8) * RT * T && wn < (SILU ? I : N);
+  float sc = 0.0f, scu = 0.0f, yold = 0.0f;
   if (writer) {
-    sc = F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[wn]) : static_cast<const float*>(scale)[wn];
-    if (beta != 0.0f) yold = y[static_cast<int64_t>(wt) * N + wn];
+    auto load_scale = [&](int n) {
+      return F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[n]) : static_cast<const float*>(scale)[n];
+    };
+    sc = load_scale(wn);
+    if (SILU) scu = load_scale(I + wn);
+    if (!SILU && beta != 0.0f) yold = y[static_cast<int64_t>(wt) * N + wn];
   }
   const int8_t* wr[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-    wr[rt] = w8 + static_cast<int64_t>(min(r0 + 8 * rt + r, N - 1)) * ldw + 64 * h + 16 * g;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = SILU ? min(a0 + 4 * rt + (r & 3), I - 1) + (r >= 4 ? I : 0) : min(r0 + 8 * rt + r, N - 1);
+    wr[rt] = w8 + static_cast<int64_t>(row) * ldw + 64 * h + 16 * g;
+  }
   const bool tok = r < T;
   const half_t* xr = x + static_cast<int64_t>(tok ? r : 0) * K + 64 * h + 16 * g;
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -692,10 +708,21 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
   }
   __syncthreads();
   if (writer) {
-    float v = 0.0f;
+    if constexpr (SILU) {
+      const int gi = 8 * (wj / 4) + (wj % 4);  // the gate row's slot; the up row's is gi + 4
+      float vg = 0.0f, vu = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][threadIdx.x % (8 * RT)];
-    y[static_cast<int64_t>(wt) * N + wn] = v * sc + (beta != 0.0f ? beta * yold : 0.0f);
+      for (int ww = 0; ww < WAVES; ++ww) vg += red[ww][wt][gi];
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww) vu += red[ww][wt][gi + 4];
+      const float gate = vg * sc + 0.0f, up = vu * scu + 0.0f;  // the plain form's y values
+      reinterpret_cast<half_t*>(y)[static_cast<int64_t>(wt) * I + wn] = f16_of_product(gate / (1.0f + expf(-gate)), up);
+    } else {
+      float v = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww) v += red[ww][wt][wj];
+      y[static_cast<int64_t>(wt) * N + wn] = v * sc + (beta != 0.0f ? beta * yold : 0.0f);
+    }
   }
 }
 
@@ -734,6 +761,26 @@ int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x,
 int even_rows(int n, int cap) {
   const int k = (n + 256 * cap - 1) / (256 * cap);
   return (n + 256 * k - 1) / (256 * k);
+}
+
+// gemv_int8_m8_kernel's SiLU form with the row grouping launch() below gives the plain
+// product at this T (same sums); only where launch() takes that kernel (T <= 8).
+template <bool F16_SCALE>
+int launch_m8_silu(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, half_t* act, int T, int K,
+                   int I, hipStream_t s) {
+  const int N = 2 * I;
+  float* out = reinterpret_cast<float*>(act);
+  if (m8_takes(T, K, N)) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 1, true>), dim3((I + 3) / 4),
+                                     dim3(8 * kWave), 0, s, w8, ldw, scale, x, out, T, K, N, 0.0f));
+  } else if (T >= 5 && N >= 14336) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 4, true>), dim3((I + 15) / 16),
+                                     dim3(8 * kWave), 0, s, w8, ldw, scale, x, out, T, K, N, 0.0f));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 2, true>), dim3((I + 7) / 8),
+                                     dim3(8 * kWave), 0, s, w8, ldw, scale, x, out, T, K, N, 0.0f));
+  }
+  return 0;
 }
 
 template <bool F16_SCALE>
@@ -931,6 +978,22 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
   const half_t* xh = static_cast<const half_t*>(x);
   return scale_is_f16 ? launch<true>(w8, ldw, scale, xh, y, T, K, N, beta, s)
                       : launch<false>(w8, ldw, scale, xh, y, T, K, N, beta, s);
+}
+
+extern "C" int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16,
+                                         const void* x, void* act, int T, int K, int I, void* stream) {
+  RH_REQUIRE(T >= 1 && T <= 8, "gemv_int8_gate_up_silu: T must be in 1..8");
+  RH_REQUIRE(K > 0 && I > 0 && K % 16 == 0, "gemv_int8_gate_up_silu: K must be a positive multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
+             "gemv_int8_gate_up_silu: ldw must be >= K, < 2^21 and a multiple of 16");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemv_int8_gate_up_silu: W8 and x must be 16-byte aligned");
+  RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr && act != nullptr, "gemv_int8_gate_up_silu: missing pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const half_t* xh = static_cast<const half_t*>(x);
+  half_t* a = static_cast<half_t*>(act);
+  return scale_is_f16 ? launch_m8_silu<true>(w8, ldw, scale, xh, a, T, K, I, s)
+                      : launch_m8_silu<false>(w8, ldw, scale, xh, a, T, K, I, s);
 }
 
 extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }

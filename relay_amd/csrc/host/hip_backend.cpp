@@ -677,6 +677,12 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       if (ks) {
         RH_CHECK(rh_w8_merge_silu(split_ws_.p, ks, T, I, L.w_gate_up.scale.p, act_.p, stream_));
         act_ready = true;
+      } else if (L.w_gate_up.i8.p && T <= 8 && H % 16 == 0) {
+        // gemm()'s product at this T (the int8 GEMV) with SiLU·mul in its epilogue: one
+        // launch fewer per layer, the same bits.
+        RH_CHECK(rh_gemv_int8_gate_up_silu(L.w_gate_up.i8.p, L.w_gate_up.ldw, L.w_gate_up.scale.p, 0, xn_.p, act_.p,
+                                           T, H, I, stream_));
+        act_ready = true;
       } else {
         gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
       }

@@ -333,3 +333,41 @@ def test_fused_qkv_matches_the_chain(torch_mod, dev, T, heads, kvh, D, H, bs, wi
         else:
             diff = np.abs(a.astype(np.int32) - b.astype(np.int32))
             assert diff.max() <= 1 and (np.sign(a) == np.sign(b)).all(), name
+
+
+@pytest.mark.parametrize("T,I,K,f16_scale", [(1, 5632, 2048, False), (3, 5632, 2048, True), (8, 5632, 2048, False),
+                                             (1, 14336, 4096, False), (4, 14336, 4096, False),
+                                             (5, 14336, 4096, True), (8, 14336, 4096, False), (6, 1536, 576, False),
+                                             (2, 102, 160, False), (7, 250, 4096, True)])
+def test_gate_up_silu_equals_the_chain(torch_mod, dev, T, I, K, f16_scale):
+    """rh_gemv_int8_gate_up_silu gives the bytes of rh_gemv_int8 over the fused [gate; up]
+    matrix followed by rh_silu_mul, at every row grouping rh_gemv_int8 takes at 1-8 tokens
+    (8, 16 and 32 rows per workgroup) and for I not a multiple of 4."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    w8, scale, x = make(2 * I, K, T, seed=T * 31 + I + K)
+    gu = run(torch, dev, w8, scale, x, f16_scale=f16_scale)
+    GU = torch.from_numpy(gu).to(dev)
+    act_a = torch.empty((T, I), dtype=torch.int16, device=dev)
+    _lib.check(L.rh_silu_mul(GU.data_ptr(), T, I, act_a.data_ptr(), None), "rh_silu_mul")
+    W = torch.from_numpy(w8).to(dev)
+    S = (torch.from_numpy(f16_bits(scale).view(np.int16)) if f16_scale else torch.from_numpy(scale)).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    act_b = torch.full((T, I), 0x7E00, dtype=torch.int16, device=dev)
+    print(f"gate_up_silu case: T={T} I={I} K={K} f16_scale={f16_scale}", flush=True)
+    _lib.check(L.rh_gemv_int8_gate_up_silu(W.data_ptr(), K, S.data_ptr(), int(f16_scale), X.data_ptr(),
+                                           act_b.data_ptr(), T, K, I, None), "rh_gemv_int8_gate_up_silu")
+    torch.cuda.synchronize()
+    assert np.array_equal(act_a.cpu().numpy(), act_b.cpu().numpy())
+
+
+def test_gate_up_silu_limits(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_int8_gate_up_silu(None, 64, None, 0, None, None, 9, 64, 32, None) != 0
+    assert "T must be in 1..8" in _lib.last_error()
+    assert L.rh_gemv_int8_gate_up_silu(None, 64, None, 0, None, None, 4, 64, 32, None) != 0
+    assert "missing pointer" in _lib.last_error()
