@@ -41,6 +41,16 @@ constexpr int kWave = 64;
 
 // fp16(fp32(a * b)): the empty asm makes the rounded fp32 product opaque, so the conversion
 // cannot be fused into a single-rounding v_fma_mix (it emits no instruction).
+// fp32(a * b), opaque to the compiler: device code compiles with fp contraction on, so an add
+// after a product may otherwise be fused with it into one fma in one kernel and not in
+// another. The merges of split products scale the merged sum with this, then add (the
+// residual, beta y), so every kernel that merges the same partials gives the same bits.
+__device__ __forceinline__ float mul_rounded(float a, float b) {
+  float p = a * b;
+  asm("" : "+v"(p));
+  return p;
+}
+
 __device__ __forceinline__ half_t f16_of_product(float a, float b) {
   float p = a * b;
   asm("" : "+v"(p));

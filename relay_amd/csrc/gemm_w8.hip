@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void w8_split_merge_kernel(const float* __rest
 #pragma unroll
     for (int z = 0; z < kMaxW8Split; ++z)
       if (z < ksn) v += p[z][e];
-    const float o = v * scale[n + e];
+    const float o = mul_rounded(v, scale[n + e]);
     y[i4 + e] = o + (beta != 0.0f ? beta * y[i4 + e] : 0.0f);
   }
 }
@@ -108,7 +108,7 @@ __device__ __forceinline__ void w8_write_out(const float16v (&acc)[AN][BT], int 
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (n + r < N) {
-          const float o = v[r] * scale[n + r];
+          const float o = mul_rounded(v[r], scale[n + r]);
           yp[n + r] = o + (beta != 0.0f ? beta * yp[n + r] : 0.0f);
         }
     }

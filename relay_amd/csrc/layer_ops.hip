@@ -153,7 +153,7 @@ __device__ __forceinline__ float4 merged4(const float* ws, int ksn, int64_t plan
 #pragma unroll
   for (int z = 0; z < kMaxMergeSplit; ++z)
     if (z < ksn) v = float4{v.x + p[z].x, v.y + p[z].y, v.z + p[z].z, v.w + p[z].w};
-  return float4{v.x * sc[0], v.y * sc[1], v.z * sc[2], v.w * sc[3]};
+  return float4{mul_rounded(v.x, sc[0]), mul_rounded(v.y, sc[1]), mul_rounded(v.z, sc[2]), mul_rounded(v.w, sc[3])};
 }
 
 // act = silu(gate) * up of the merged gate_up product (rows [0, I) gate, [I, 2I) up), the

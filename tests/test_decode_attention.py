@@ -184,3 +184,44 @@ def test_rejects_unsupported_shapes(torch_mod, dev):
     rc = L.rh_paged_decode_attention(None, 256, None, None, None, None, 1, 4, 4, 64, 16, 100, 1, 0.1, None, None, None,
                                      None, 256, None)
     assert rc != 0 and "slice_keys" in _lib.last_error()
+
+
+def test_slice_merge_is_stable_over_many_launches(torch_mod, dev):
+    """The last-arriving workgroup of each (sequence, kv head) merges the other slices'
+    partials through relaxed device-scope accesses ordered only by waiting for its own stores
+    before the counter increment. A merge that read a stale partial would change the output
+    of some launch: 300 back-to-back launches at config 2's shape with 512-key slices (4
+    partials per group) must give the first launch's bits every time, and that must match
+    the oracle."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    case = PagedCase([2048] * 32, 1, 32, 4, 64, 16, seed=3, extra_blocks=0)
+    d = case.to_device(torch, dev)
+    H, KVH, D, n, sk = 32, 4, 64, 32, 512
+    parts = 4
+    dec = torch.from_numpy(case.dec_meta()).to(dev)
+    part_o = torch.empty(n * H * parts * D, device=dev)
+    part_ml = torch.empty(n * H * parts * 2, device=dev)
+    ctr = torch.zeros(n * KVH, dtype=torch.int32, device=dev)
+    outs = [torch.empty((n, H * D), dtype=torch.float16, device=dev) for _ in range(2)]
+    L = _lib.lib()
+    print("decode merge stability: 32 x 2048, 512-key slices, 300 launches", flush=True)
+
+    def launch(out):
+        _lib.check(L.rh_paged_decode_attention(d["q"].data_ptr(), H * D, d["k"].data_ptr(), d["v"].data_ptr(),
+                                               dec.data_ptr(), d["tables"].data_ptr(), n, H, KVH, D, 16, sk, parts,
+                                               1.0 / math.sqrt(D), part_o.data_ptr(), part_ml.data_ptr(),
+                                               ctr.data_ptr(), out.data_ptr(), H * D, None), "decode")
+
+    launch(outs[0])
+    torch.cuda.synchronize()
+    check_close(outs[0].cpu().numpy().astype(np.float32), oracle_out(case))
+    first = outs[0].clone()
+    bad = torch.zeros((), dtype=torch.int32, device=dev)
+    for i in range(300):
+        launch(outs[1])
+        bad += (outs[1].view(torch.int16) != first.view(torch.int16)).any().to(torch.int32)
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0, f"{int(bad.item())} of 300 launches differed from the first"
+    assert int(ctr.abs().sum().item()) == 0
