@@ -169,9 +169,10 @@ int rh_gemv_int8_max_tokens(void);
  * rh_gemv_f16_rmsnorm, rh_gemv_f16_silu, rh_gemv_f16_qkv and rh_gemv_f16_rmsnorm_qkv, with
  * their operands and limits (rh_gemv_f16_fused_fits(T, K) for the fused producers) and
  * rh_gemv_int8's weights and scales. At 9-16 tokens each gives the bits of the launches it
- * replaces (both run the 16-row tile); at 1-8 tokens the plain rh_gemv_int8 runs the
- * whole-line kernel, which adds in another order, and the two agree within the fp32
- * accumulation bound 4 * K * 2^-24 * sum|w * x|. */
+ * replaces (both run the 16-row tile); at 1-8 tokens the plain rh_gemv_int8 and the RMSNorm
+ * and qkv forms run whole-line kernels that split K over a different number of waves, and
+ * rh_gemv_int8_silu runs the 16-row tile, so there the fused results agree with the
+ * launches they replace within the fp32 accumulation bound 4 * K * 2^-24 * sum|w * x|. */
 int rh_gemv_int8_rmsnorm(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
                          const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream);
 int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* gu, float* y,

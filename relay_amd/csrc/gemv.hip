@@ -843,6 +843,146 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
               : launch_nb<4, 1, F16_SCALE>(w8, ldw, scale, x, y, T, K, N, beta, s);
 }
 
+// gemv_int8_m8_kernel's whole-line form with a fused producer and/or the qkv epilogue, for 1-8
+// tokens: 16 rows per workgroup as two 8-row groups (kRope: the RoPE pairs of rope_tile_row, so
+// both halves of every pair end in one workgroup), waves splitting K in runs of 128, the
+// activations read as for the plain form (kPlain) or normalised once per workgroup into LDS
+// (kRmsNorm, stage_operands: rows K + 8 halves apart, so the 16 lanes of a B read cover 8
+// tokens x 2 halves on distinct banks). One writer thread per (token, row) sums the waves'
+// partials in a fixed order; kRope writers take a pair (m, m + 8) and apply qkv_post's
+// arithmetic (rope_epilogue's float operations).
+template <int WAVES, int DEPTH, bool F16_SCALE, int PRO, int EPI>
+__global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
+    const int8_t* __restrict__ w8, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
+    const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
+  static_assert(PRO == kPlain || PRO == kRmsNorm, "the whole-line fused form takes RMSNorm or no producer");
+  constexpr int RT = 2;
+  __shared__ float red[WAVES][8][8 * RT];
+  __shared__ float s_inv[8];
+  __shared__ int s_pos[EPI == kRope ? 8 : 1];
+  __shared__ int64_t s_kvrow[EPI == kRope ? 8 : 1];
+  extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // kRmsNorm: [T][K + 8]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int r = c >> 1, h = c & 1;  // A row: row r of group rt, half h; B column: token r, half h
+  auto out_row = [&](int rt, int m) {  // m < 8: row m of group rt
+    return EPI == kRope ? rope_tile_row(blockIdx.x, 8 * rt + m, ra.D) : 16 * blockIdx.x + 8 * rt + m;
+  };
+  const int nsteps = (K + 127) / 128;
+  const int per = (nsteps + WAVES - 1) / WAVES;
+  const int s0 = w * per, s1 = min(nsteps, s0 + per);
+  const int8_t* wr[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    wr[rt] = w8 + static_cast<int64_t>(min(out_row(rt, r), N - 1)) * ldw + 64 * h + 16 * g;
+  const bool tok = r < T;
+  const half_t* xr = static_cast<const half_t*>(xin) + static_cast<int64_t>(tok ? r : 0) * K + 64 * h + 16 * g;
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint4v wv[DEPTH][RT];
+  auto load_w = [&](int st) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int k = (st + d) * 128 + 64 * h + 16 * g;
+      const bool live = st + d < s1 && k < K;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        wv[d][rt] = live ? *reinterpret_cast<const uint4v*>(wr[rt] + (st + d) * 128) : uint4v{0u, 0u, 0u, 0u};
+    }
+  };
+  load_w(s0);  // the first weights are in flight under the prologue
+  if (PRO == kRmsNorm) stage_operands<PRO, WAVES, WAVES >= 16 ? 4 : 8>(xin, norm_w, eps, T, K, sxb, s_inv);
+  if (EPI == kRope && w == WAVES - 1) rope_lookups(ra, blockIdx.x, T, lane, s_pos, s_kvrow);
+  float4v acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int st = s0; st < s1; st += DEPTH) {
+    if (st != s0) load_w(st);
+    half8 xa[DEPTH], xb[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int k = (st + d) * 128 + 64 * h + 16 * g;
+      const bool live = st + d < s1 && k < K;
+      if (PRO == kPlain) {
+        xa[d] = live && tok ? load_half8(xr + (st + d) * 128) : zero;
+        xb[d] = live && tok ? load_half8(xr + (st + d) * 128 + 8) : zero;
+      } else {
+        const half_t* xs = sxb + (tok ? r : 0) * (K + 8) + k;
+        xa[d] = live && tok ? *reinterpret_cast<const half8*>(xs) : zero;
+        xb[d] = live && tok ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]), xa[d], acc[rt]);
+        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]), xb[d], acc[rt]);
+      }
+  }
+  // Lane (column 2t + h, g) holds C rows 4g + q = (row 2g + q / 2, half q % 2).
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float m0 = h ? acc[rt][1] : acc[rt][0], m1 = h ? acc[rt][3] : acc[rt][2];
+    const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
+    if (h == 0 && tok) {
+      red[w][r][8 * rt + 2 * g] = v0;
+      red[w][r][8 * rt + 2 * g + 1] = v1;
+    }
+  }
+  __syncthreads();
+  auto row_scale = [&](int n) {
+    return F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[n]) : static_cast<const float*>(scale)[n];
+  };
+  // The scaled sum of (token t, slot m = 8 rt + row) as the plain product stores it.
+  auto value = [&](int t, int m) {
+    float v = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < WAVES; ++ww) v += red[ww][t][m];
+    return v * row_scale(min(out_row(m >> 3, m & 7), N - 1));
+  };
+  if constexpr (EPI == kStore) {
+    const int t = threadIdx.x / 16, m = threadIdx.x % 16;
+    const int n = 16 * blockIdx.x + m;
+    if (threadIdx.x < 16 * T && n < N) {
+      float* dst = y + static_cast<int64_t>(t) * N + n;
+      *dst = value(t, m) + (beta != 0.0f ? beta * *dst : 0.0f);
+    }
+  } else {
+    const int t = threadIdx.x / 8, m = threadIdx.x % 8;  // the pair (m, m + 8)
+    if (threadIdx.x >= 8 * T) return;
+    const int D = ra.D, tph = D / 16, hd = blockIdx.x / tph, j0 = (blockIdx.x - hd * tph) * 8;
+    const int ja = j0 + m, jb = D / 2 + j0 + m;
+    float a = value(t, m) + 0.0f, b = value(t, m + 8) + 0.0f;
+    if (ra.bias) {
+      a += ra.bias[hd * D + ja];
+      b += ra.bias[hd * D + jb];
+    }
+    const int p = s_pos[t];
+    if (hd < ra.heads + ra.kv_heads) {
+      const float angle = static_cast<float>(p) * ra.inv_freq[ja];
+      float sn, cs;
+      sincosf(angle, &sn, &cs);
+      const float ra_ = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+      const float rb_ = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
+      a = ra_;
+      b = rb_;
+    }
+    y[static_cast<int64_t>(t) * N + hd * D + ja] = a;
+    y[static_cast<int64_t>(t) * N + hd * D + jb] = b;
+    if (hd < ra.heads) {
+      if (ra.q_out) {
+        half_t* q = ra.q_out + static_cast<int64_t>(t) * ra.heads * D + hd * D;
+        q[ja] = f16_of_product(a, ra.q_scale);
+        q[jb] = f16_of_product(b, ra.q_scale);
+      }
+    } else {
+      half_t* dst = (hd < ra.heads + ra.kv_heads ? ra.kc : ra.vc) + s_kvrow[t];
+      dst[ja] = static_cast<half_t>(a);
+      dst[jb] = static_cast<half_t>(b);
+    }
+  }
+}
+
 // The int8 product with a fused producer (PRO) and/or the qkv epilogue (EPI): 16-row
 // workgroups with the wave count of the 16-row tile's plain launch for the same N, so at
 // 9-16 tokens the sums are the plain product's bit for bit; at 1-8 tokens the plain product
@@ -852,9 +992,23 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
                  float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
-  // Fused launches keep the 16-row tile at 1-8 tokens too (a one-token vector-ALU form
-  // behind the producers made TinyLlama int8 decode steps slower).
   const int tiles = (N + 15) / 16;
+  // 1-8 tokens without the SiLU producer: the whole-line form (a one-token vector-ALU form
+  // behind the producers made TinyLlama int8 decode steps slower).
+  if constexpr (PRO != kSiluMul) {
+    if (T <= 8) {
+      if (tiles < 256) {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, F16_SCALE, PRO, EPI>), dim3(tiles),
+                                         dim3(16 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
+                                         beta, ra));
+      } else {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, F16_SCALE, PRO, EPI>), dim3(tiles),
+                                         dim3(8 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
+                                         beta, ra));
+      }
+      return 0;
+    }
+  }
   if constexpr (PRO == kPlain) {
     if (T > kMaxTokens) {  // the qkv epilogue alone, 17-32 tokens: two column blocks
       if (tiles < 256) {
