@@ -402,11 +402,19 @@ int oracle_rope_inv_freq(const OracleConfig* cfg, float* out) {
 }
 
 void oracle_f32_to_f16(const float* in, std::uint16_t* out, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 16))
   for (size_t i = 0; i < n; ++i) out[i] = to_f16(in[i]);
 }
 
 void oracle_f16_to_f32(const std::uint16_t* in, float* out, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 16))
   for (size_t i = 0; i < n; ++i) out[i] = from_f16(in[i]);
+}
+
+// a[i] = the fp32 value of fp16(a[i]) (to_f16, then exact widening), in place.
+void oracle_round_f16_inplace(float* a, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 16))
+  for (size_t i = 0; i < n; ++i) a[i] = from_f16(to_f16(a[i]));
 }
 
 // The host int8 quantizer of cuda_backend.cu:282-304: per row, scale = max|w| / 127

@@ -39,6 +39,7 @@ def lib() -> C.CDLL:
             "oracle_rope_inv_freq": (I, [P, P]),
             "oracle_f32_to_f16": (None, [P, P, SZ]),
             "oracle_f16_to_f32": (None, [P, P, SZ]),
+            "oracle_round_f16_inplace": (None, [P, SZ]),
             "oracle_quantize_int8": (None, [P, I, I, P, P]),
             "oracle_paged_attention": (None, [P, C.c_long, P, P, P, P, P, P, P, I, I, I, I, I, F, P]),
             "oracle_paged_attention_f64": (None, [P, C.c_long, P, P, P, P, P, P, P, I, I, I, I, I, D, P]),
@@ -198,6 +199,13 @@ def f32_to_f16(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.shape, np.uint16)
     lib().oracle_f32_to_f16(x.ctypes.data, out.ctypes.data, x.size)
     return out
+
+
+def round_f16_inplace(a: np.ndarray) -> np.ndarray:
+    """a <- fp16(a) as fp32 values (round to nearest even), in place; a is C-contiguous fp32."""
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    lib().oracle_round_f16_inplace(a.ctypes.data, a.size)
+    return a
 
 
 def f16_to_f32(h: np.ndarray) -> np.ndarray:

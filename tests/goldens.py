@@ -75,7 +75,11 @@ def prompt_of(name: str) -> list:
 def _to_f16_values(a):
     if a is None:
         return None
-    np.copyto(a, a.astype(np.float16).astype(np.float32))  # RNE, in place
+    import oracle as O
+
+    # RNE, in place: the oracle's conversion (equal to numpy's cast, test_oracle.py), which
+    # allocates nothing and runs on every core
+    O.round_f16_inplace(a)
     return a
 
 
@@ -83,10 +87,14 @@ _WEIGHTS_CACHE = {}
 
 
 def weights_for(name: str) -> HostWeights:
-    """The golden's weights (the last ones built are kept: goldens of one shape share them)."""
+    """The golden's weights (the two last used are kept: goldens of one shape share them, and
+    the test order alternates between the TinyLlama and Llama-3 shapes; at most ~7 GB)."""
     key = (repr(config_of(name)), name in FP16_WEIGHTS)
-    if key not in _WEIGHTS_CACHE:
-        _WEIGHTS_CACHE.clear()
+    if key in _WEIGHTS_CACHE:
+        _WEIGHTS_CACHE[key] = _WEIGHTS_CACHE.pop(key)  # most recently used last
+    else:
+        while len(_WEIGHTS_CACHE) >= 2:
+            del _WEIGHTS_CACHE[next(iter(_WEIGHTS_CACHE))]
         _WEIGHTS_CACHE[key] = _build_weights(name)
     return _WEIGHTS_CACHE[key]
 

@@ -125,6 +125,16 @@ def test_f32_to_f16_is_ieee_round_to_nearest_even():
     assert np.array_equal(O.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
 
 
+def test_round_f16_inplace_is_numpys_cast_round_trip():
+    x = special_floats()
+    y = O.round_f16_inplace(x.copy())
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(y), nan)
+    assert np.array_equal(y[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
 @needs_ref
 def test_f32_to_f16_equals_the_reference_build():
     import ctypes as C
