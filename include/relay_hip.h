@@ -195,6 +195,17 @@ int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, i
 int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
                               void* act, int T, int K, int I, void* stream);
 
+/* rh_gemv_int8_gate_up_silu with relay's RMSNorm of x folded in: act[t, a] = fp16(silu(g) *
+ * u) of the product with xn = fp16(norm_w * (x * 1/sqrt(mean(x^2) + eps))), x fp32 [T, K] (the
+ * residual stream), norm_w fp32 [K], 1 <= T <= 8, T * (K + 8) * 2 bytes <= 64 KiB. Where the
+ * launch has >= 256 workgroups (I >= 2041) the bytes equal rh_rmsnorm followed by
+ * rh_gemv_int8_gate_up_silu; below that the waves split K differently and the sums agree
+ * within the fp32 accumulation bound. Every workgroup normalises x itself, so this pays
+ * only while the (I + 7) / 8 workgroups fit one round on the CUs. No counterpart in relay
+ * (rms_norm_kernel, gemm and silu_mul_kernel, cuda_backend.cu:587-589). */
+int rh_gemv_int8_rmsnorm_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
+                                      const float* norm_w, float eps, void* act, int T, int K, int I, void* stream);
+
 /* y[t, n] = sum_k W16[n, k] * x[t, k]  (+ beta * y[t, n] when beta != 0), for 1 <= T <= 32:
  * the dense projection at decode batch sizes. W16 fp16 [N, K] rows ldw elements apart
  * (ldw >= K, a multiple of 8); x fp16 [T, K]; y fp32 [T, N]; K a multiple of 16; W16 and x

@@ -81,7 +81,7 @@ enum Prologue { kPlain = 0, kRmsNorm = 1, kSiluMul = 2 };
 // k and v into the paged cache as fp16, q as fp16). For kRope the tile of workgroup i
 // holds rows (h D + j0 + r, h D + D/2 + j0 + r), r < 8, of head h = i / (D/16),
 // j0 = 8 (i % (D/16)), so both halves of every RoPE pair end in one wave.
-enum Epilogue { kStore = 0, kRope = 1 };
+enum Epilogue { kStore = 0, kRope = 1, kSilu = 2 };  // kSilu: the int8 whole-line fused form only
 
 struct RopeArgs {
   const float* bias;  // [N] or null
@@ -865,7 +865,9 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int r = c >> 1, h = c & 1;  // A row: row r of group rt, half h; B column: token r, half h
-  auto out_row = [&](int rt, int m) {  // m < 8: row m of group rt
+  const int I = N / 2, a0 = 8 * blockIdx.x;  // kSilu only
+  auto out_row = [&](int rt, int m) -> int {  // m < 8: row m of group rt
+    if (EPI == kSilu) return min(a0 + 4 * rt + (m & 3), I - 1) + (m >= 4 ? I : 0);
     return EPI == kRope ? rope_tile_row(blockIdx.x, 8 * rt + m, ra.D) : 16 * blockIdx.x + 8 * rt + m;
   };
   const int nsteps = (K + 127) / 128;
@@ -946,6 +948,15 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     if (threadIdx.x < 16 * T && n < N) {
       float* dst = y + static_cast<int64_t>(t) * N + n;
       *dst = value(t, m) + (beta != 0.0f ? beta * *dst : 0.0f);
+    }
+  } else if constexpr (EPI == kSilu) {
+    // Thread (t, j) writes act[t, a0 + j]: gate slot 8 (j / 4) + j % 4, up slot 4 further
+    // (gemv_int8_m8_kernel's SiLU epilogue arithmetic).
+    const int t = threadIdx.x / 8, j = threadIdx.x % 8, a = a0 + j;
+    if (threadIdx.x < 8 * T && a < I) {
+      const int gi = 8 * (j / 4) + j % 4;
+      const float gate = value(t, gi) + 0.0f, up = value(t, gi + 4) + 0.0f;
+      reinterpret_cast<half_t*>(y)[static_cast<int64_t>(t) * I + a] = f16_of_product(gate / (1.0f + expf(-gate)), up);
     }
   } else {
     const int t = threadIdx.x / 8, m = threadIdx.x % 8;  // the pair (m, m + 8)
@@ -1054,6 +1065,29 @@ int check_rope(const float* inv_freq, const int* pos, const int* seq, const int*
   return 0;
 }
 
+// act = SiLU(gate) * up of the int8 gate/up product of RMSNorm(x), 1-8 tokens: the fused
+// whole-line kernel with both prologue and SiLU epilogue (16 weight rows = 8 outputs per
+// workgroup). With >= 256 workgroups it runs 8 waves of 2 steps, the K split of
+// gemv_int8_m8_kernel, so the bytes equal rh_rmsnorm followed by rh_gemv_int8_gate_up_silu.
+template <bool F16_SCALE>
+int launch_m8_rmsnorm_silu(const int8_t* w8, int64_t ldw, const void* scale, const float* x, const float* norm_w,
+                           float eps, half_t* act, int T, int K, int I, hipStream_t s) {
+  const size_t staged = static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
+  RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
+  const int tiles = (I + 7) / 8, N = 2 * I;
+  float* out = reinterpret_cast<float*>(act);
+  if (tiles < 256) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
+                                     dim3(16 * kWave), staged, s, w8, ldw, scale, x, norm_w, eps, out, T, K, N, 0.0f,
+                                     RopeArgs{}));
+  } else {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
+                                     dim3(8 * kWave), staged, s, w8, ldw, scale, x, norm_w, eps, out, T, K, N, 0.0f,
+                                     RopeArgs{}));
+  }
+  return 0;
+}
+
 template <int PRO, int EPI>
 int int8_fused(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* xin,
                const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream,
@@ -1148,6 +1182,24 @@ extern "C" int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const vo
   half_t* a = static_cast<half_t*>(act);
   return scale_is_f16 ? launch_m8_silu<true>(w8, ldw, scale, xh, a, T, K, I, s)
                       : launch_m8_silu<false>(w8, ldw, scale, xh, a, T, K, I, s);
+}
+
+extern "C" int rh_gemv_int8_rmsnorm_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16,
+                                                 const float* x, const float* norm_w, float eps, void* act, int T,
+                                                 int K, int I, void* stream) {
+  RH_REQUIRE(T >= 1 && T <= 8, "gemv_int8_rmsnorm_gate_up_silu: T must be in 1..8");
+  RH_REQUIRE(K > 0 && I > 0 && K % 16 == 0, "gemv_int8_rmsnorm_gate_up_silu: K must be a positive multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
+             "gemv_int8_rmsnorm_gate_up_silu: ldw must be >= K, < 2^21 and a multiple of 16");
+  RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr && norm_w != nullptr && act != nullptr,
+             "gemv_int8_rmsnorm_gate_up_silu: missing pointer");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w8) | reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(norm_w)) %
+                     16 == 0,
+             "gemv_int8_rmsnorm_gate_up_silu: W8, x and the norm weights must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  half_t* a = static_cast<half_t*>(act);
+  return scale_is_f16 ? launch_m8_rmsnorm_silu<true>(w8, ldw, scale, x, norm_w, eps, a, T, K, I, s)
+                      : launch_m8_rmsnorm_silu<false>(w8, ldw, scale, x, norm_w, eps, a, T, K, I, s);
 }
 
 extern "C" int rh_gemv_f16_max_tokens(void) { return 2 * kMaxTokens; }

@@ -363,6 +363,58 @@ def test_gate_up_silu_equals_the_chain(torch_mod, dev, T, I, K, f16_scale):
     assert np.array_equal(act_a.cpu().numpy(), act_b.cpu().numpy())
 
 
+@pytest.mark.parametrize("T,I,K,f16_scale", [(1, 5632, 2048, False), (4, 5632, 2048, True), (8, 5632, 2048, False),
+                                             (1, 14336, 4096, False), (7, 14336, 4096, True), (3, 1536, 576, False),
+                                             (2, 102, 160, False), (5, 250, 4096, True), (8, 2048, 64, False)])
+def test_rmsnorm_gate_up_silu_matches_the_chain(torch_mod, dev, T, I, K, f16_scale):
+    """rh_gemv_int8_rmsnorm_gate_up_silu against rh_rmsnorm -> rh_gemv_int8_gate_up_silu: the
+    same bytes where the fused launch has >= 256 workgroups (the same K split); below that,
+    within the chain's fp32 accumulation bound carried through SiLU·mul plus one fp16
+    rounding."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(T * 131 + I + K)
+    w8, scale, _ = make(2 * I, K, T, seed=T * 31 + I + K + 1)
+    W = torch.from_numpy(w8).to(dev)
+    S = (torch.from_numpy(f16_bits(scale).view(np.int16)) if f16_scale else torch.from_numpy(scale)).to(dev)
+    x = torch.from_numpy((rng.standard_normal((T, K)) * 3).astype(np.float32)).to(dev)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).to(dev)
+    xn = torch.empty((T, K), dtype=torch.int16, device=dev)
+    act_a = torch.empty((T, I), dtype=torch.int16, device=dev)
+    act_b = torch.full((T, I), 0x7E00, dtype=torch.int16, device=dev)
+    print(f"rmsnorm_gate_up_silu case: T={T} I={I} K={K} f16_scale={f16_scale}", flush=True)
+    _lib.check(L.rh_rmsnorm(x.data_ptr(), None, T, nw.data_ptr(), K, 1e-5, xn.data_ptr(), None), "rh_rmsnorm")
+    _lib.check(L.rh_gemv_int8_gate_up_silu(W.data_ptr(), K, S.data_ptr(), int(f16_scale), xn.data_ptr(),
+                                           act_a.data_ptr(), T, K, I, None), "rh_gemv_int8_gate_up_silu")
+    _lib.check(L.rh_gemv_int8_rmsnorm_gate_up_silu(W.data_ptr(), K, S.data_ptr(), int(f16_scale), x.data_ptr(),
+                                                   nw.data_ptr(), 1e-5, act_b.data_ptr(), T, K, I, None),
+               "rh_gemv_int8_rmsnorm_gate_up_silu")
+    torch.cuda.synchronize()
+    a, b = act_a.cpu().numpy(), act_b.cpu().numpy()
+    if (I + 7) // 8 >= 256:
+        assert np.array_equal(a, b)
+    else:
+        xb = xn.cpu().numpy().view(np.uint16)
+        s_used = bits_to_f32(f16_bits(scale)) if f16_scale else scale
+        exact = O.gemv_int8(w8, s_used, xb).astype(np.float64)
+        err = bound(w8, s_used, xb) + 2 * EPS32 * np.abs(exact)
+        g, u, dg, du = exact[:, :I], exact[:, I:], err[:, :I], err[:, I:]
+        silu = g / (1.0 + np.exp(-g))
+        f16_close(a, b, 1.1 * np.abs(u) * dg + np.abs(silu) * du + dg * du, "act")
+
+
+def test_rmsnorm_gate_up_silu_limits(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_int8_rmsnorm_gate_up_silu(None, 64, None, 0, None, None, 1e-5, None, 9, 64, 32, None) != 0
+    assert "T must be in 1..8" in _lib.last_error()
+    assert L.rh_gemv_int8_rmsnorm_gate_up_silu(None, 64, None, 0, None, None, 1e-5, None, 4, 64, 32, None) != 0
+    assert "missing pointer" in _lib.last_error()
+
+
 def test_gate_up_silu_limits(dev):
     from relay_amd import _lib
 
