@@ -742,6 +742,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_kernel(const int8_
 // 4096 17.7 -> 14.6.
 bool m8_takes(int T, int K, int N) { return T >= 1 && T <= 8 && (T <= 3 || std::min(K, N) <= 2048); }
 
+// 8-row workgroups that fit one round on the CUs run 16 waves of one step each: twice the
+// waves over the same K, every load of a wave issued at once (us, 8 x 2 -> 16 x 1, same
+// process: 4096 -> 1024 at T = 1 / 4 / 8 4.2 -> 4.1, 4.5 -> 4.3, 4.9 -> 4.7; 5632 -> 2048 at
+// T = 1 5.4 -> 5.1; 2048 x 2048 4.2 -> 4.2). With more workgroups than CUs 16 waves were
+// slower (4096 -> 14336 at T = 8 in 8-row groups: 20.5 against 21.5 at 8 x 2, both far
+// behind the 32-row form's 15.1).
+bool m8_one_round(int N) { return (N + 7) / 8 <= 256; }
+
 template <int NB, int RT, bool F16_SCALE>
 int launch_nb(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
               float beta, hipStream_t s, int rows_per = 16 * RT) {
@@ -770,7 +778,10 @@ int launch_m8_silu(const int8_t* w8, int64_t ldw, const void* scale, const half_
                    int I, hipStream_t s) {
   const int N = 2 * I;
   float* out = reinterpret_cast<float*>(act);
-  if (m8_takes(T, K, N)) {
+  if (m8_takes(T, K, N) && m8_one_round(N)) {
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<16, 1, F16_SCALE, 1, true>), dim3((I + 3) / 4),
+                                     dim3(16 * kWave), 0, s, w8, ldw, scale, x, out, T, K, N, 0.0f));
+  } else if (m8_takes(T, K, N)) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE, 1, true>), dim3((I + 3) / 4),
                                      dim3(8 * kWave), 0, s, w8, ldw, scale, x, out, T, K, N, 0.0f));
   } else if (T >= 5 && N >= 14336) {
@@ -787,8 +798,13 @@ template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
   if (m8_takes(T, K, N)) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE>), dim3((N + 7) / 8), dim3(8 * kWave), 0, s,
-                                     w8, ldw, scale, x, y, T, K, N, beta));
+    if (m8_one_round(N)) {
+      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<16, 1, F16_SCALE>), dim3((N + 7) / 8), dim3(16 * kWave), 0,
+                                       s, w8, ldw, scale, x, y, T, K, N, beta));
+    } else {
+      RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<8, 2, F16_SCALE>), dim3((N + 7) / 8), dim3(8 * kWave), 0, s,
+                                       w8, ldw, scale, x, y, T, K, N, beta));
+    }
     return 0;
   }
   if (T >= 5 && T <= 8 && N >= 14336) {
