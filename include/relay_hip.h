@@ -291,6 +291,17 @@ int rh_gemm_w8_split(const int8_t* w8, int64_t ldw, const float* scale, const vo
 int rh_gemm_w8_plan(int T, int K, int N);
 int rh_gemm_w8_kernel(int T, int K, int N, int ksplit);
 
+/* act[t, a] = fp16(silu(g) * u), g and u the rows a and I + a of rh_gemm_w8's product of
+ * the fused gate/up matrix W8 [2 I, K] (scale fp32 [2 I]) with x fp16 [T, K]; act fp16
+ * [T, I]. Runs the 256 x 96 tile (kernel 1 of rh_gemm_w8_kernel) unsplit with each
+ * workgroup holding the gate and up rows of 128 outputs, so where rh_gemm_w8_kernel(T, K,
+ * 2 I, 1) is 1 the bytes equal rh_gemm_w8 into an fp32 [T, 2 I] buffer followed by
+ * rh_silu_mul, in one launch and without the fp32 buffer. Requires (I + 256) * ldw < 2^31.
+ * No counterpart in relay (dequantize + cublasGemmEx, then silu_mul_kernel,
+ * cuda_backend.cu:588-589, 718-722). */
+int rh_gemm_w8_gate_up_silu(const int8_t* w8, int64_t ldw, const float* scale, const void* x, void* act, int T, int K,
+                            int I, void* stream);
+
 /* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 32-token tile (64 tokens above 32) and K cut
  * into ksplit ranges (1 <= ksplit <= 8, at most K / 64), so that decode batches of 17-64
  * tokens read the int8 weights once on enough workgroups; workspace as for

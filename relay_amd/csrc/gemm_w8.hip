@@ -132,13 +132,20 @@ __device__ __forceinline__ void w8_write_out(const float16v (&acc)[AN][BT], int 
   }
 }
 
-template <int AN, int BT, int WPE>
+// SILU (AN = 2, one K range): W is the fused [gate; up] matrix (N = 2 I rows) and the tile
+// holds the 128 outputs a0 .. a0 + 127 (a0 = 128 x its row index): block 0 of wave w gate
+// rows a0 + 32 w .. +32, block 1 the up rows I rows further, so every accumulator register
+// of block 0 has its partner at the same place in block 1 and the epilogue writes act[t, a]
+// = fp16(silu(g) * u) (fp16 [T, I]) instead of y -- the values of the plain product
+// followed by silu_mul_vec_kernel.
+template <int AN, int BT, int WPE, bool SILU = false>
 __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restrict__ w8, int64_t ldw,
                                                            const float* __restrict__ scale,
                                                            const half_t* __restrict__ x, float* y, int T, int K, int N,
                                                            float beta, float* ws, int n_row, int n_tok, int ksn,
                                                            int vec_out) {
-  constexpr int KS = 64, XR = KS + 8, RB = 128 * AN, TB = 32 * BT;
+  static_assert(!SILU || AN == 2, "the SiLU tile pairs gate and up blocks");
+  constexpr int KS = 64, XR = KS + 8, RB = SILU ? 128 : 128 * AN, TB = 32 * BT;
   __shared__ __attribute__((aligned(16))) half_t xs[2][TB * XR];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
   const int total = n_row * n_tok * ksn, L = blockIdx.x;
@@ -150,10 +157,12 @@ __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restr
 
   const __amdgpu_buffer_rsrc_t wrs = w8_rsrc(w8 + static_cast<int64_t>(n0) * ldw + static_cast<int64_t>(sbeg) * KS);
   const __amdgpu_buffer_rsrc_t xrs = w8_rsrc(x + static_cast<int64_t>(sbeg) * KS);
+  const int I = N / 2;  // SILU only
   int woff[AN];
 #pragma unroll
   for (int a = 0; a < AN; ++a)
-    woff[a] = (min(n0 + 32 * (AN * w + a) + c, N - 1) - n0) * static_cast<int>(ldw) + 32 * h;
+    woff[a] = SILU ? (min(n0 + 32 * w + c, I - 1) - n0 + a * I) * static_cast<int>(ldw) + 32 * h
+                   : (min(n0 + 32 * (AN * w + a) + c, N - 1) - n0) * static_cast<int>(ldw) + 32 * h;
   int xoff[BT];  // activation piece j of this thread: token e / 8, k piece e % 8, e = tid + 256 j
 #pragma unroll
   for (int j = 0; j < BT; ++j) {
@@ -263,7 +272,37 @@ __global__ __launch_bounds__(256, WPE) void w8_tile_kernel(const int8_t* __restr
     }
   }
 
-  w8_write_out<AN, BT>(acc, w, c, h, n0, t0, kz, T, N, ksn, ws, scale, y, beta, vec_out);
+  if constexpr (SILU) {
+    half_t* act = reinterpret_cast<half_t*>(y);
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      const int t = t0 + 32 * b + c;
+      if (t >= T) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int a = n0 + 32 * w + 8 * q + 4 * h;
+        half_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ar = min(a + r, I - 1);
+          // the values w8_write_out's vector store gives y (sum x scale, rounded once)
+          const float g = mul_rounded(acc[0][b][4 * q + r], scale[ar]);
+          const float u = mul_rounded(acc[1][b][4 * q + r], scale[I + ar]);
+          o[r] = f16_of_product(g / (1.0f + expf(-g)), u);
+        }
+        half_t* dst = act + static_cast<int64_t>(t) * I + a;
+        if (vec_out && a + 3 < I) {
+          *reinterpret_cast<half4*>(dst) = half4{o[0], o[1], o[2], o[3]};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (a + r < I) dst[r] = o[r];
+        }
+      }
+    }
+  } else {
+    w8_write_out<AN, BT>(acc, w, c, h, n0, t0, kz, T, N, ksn, ws, scale, y, beta, vec_out);
+  }
 }
 
 // ---- the wide-step kernel ---------------------------------------------------------------
@@ -485,6 +524,19 @@ int launch_w8_tile(const int8_t* w8, int64_t ldw, const float* scale, const half
   return 0;
 }
 
+// act = SiLU(gate) * up of the fused [gate; up] product on the 256 x 96 tile, one K range.
+int launch_w8_tile_silu(const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, half_t* act, int T, int K,
+                        int I, hipStream_t s) {
+  const int n_row = (I + 127) / 128, n_tok = (T + 95) / 96;
+  const int64_t total = static_cast<int64_t>(n_row) * n_tok;
+  RH_REQUIRE(total < (int64_t(1) << 31), "gemm_w8: grid too large");
+  const int vec_out = I % 4 == 0 && reinterpret_cast<uintptr_t>(act) % 8 == 0;
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((w8_tile_kernel<2, 3, 2, true>), dim3(static_cast<unsigned>(total)), dim3(256), 0, s,
+                                   w8, ldw, scale, x, reinterpret_cast<float*>(act), T, K, 2 * I, 0.0f, nullptr, n_row,
+                                   n_tok, 1, vec_out));
+  return 0;
+}
+
 int launch_w8_cfg(int cfg, const int8_t* w8, int64_t ldw, const float* scale, const half_t* x, float* y, int T, int K,
                   int N, float beta, hipStream_t s, int ksplit, float* ws) {
   switch (cfg) {
@@ -518,6 +570,19 @@ extern "C" int rh_gemm_w8(const int8_t* w8, int64_t ldw, const float* scale, con
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
   return launch_w8_cfg(w8_cfg_for(T, K, N, 1), w8, ldw, scale, xh, y, T, K, N, beta, st, 1, nullptr);
+}
+
+extern "C" int rh_gemm_w8_gate_up_silu(const int8_t* w8, int64_t ldw, const float* scale, const void* x, void* act,
+                                       int T, int K, int I, void* stream) {
+  if (T == 0) return 0;
+  RH_REQUIRE(I > 0, "gemm_w8_gate_up_silu: I must be positive");
+  RH_REQUIRE(w8 != nullptr && scale != nullptr && x != nullptr && act != nullptr,
+             "gemm_w8_gate_up_silu: missing pointer");
+  if (int rc = gemm_w8_checks(w8, ldw, x, T, K, 2 * I)) return rc;
+  RH_REQUIRE((static_cast<int64_t>(I) + 256) * ldw < (int64_t(1) << 31),
+             "gemm_w8_gate_up_silu: I * ldw too large for 32-bit buffer offsets");
+  return launch_w8_tile_silu(w8, ldw, scale, static_cast<const half_t*>(x), static_cast<half_t*>(act), T, K, I,
+                             static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rh_gemm_w8_plan(int T, int K, int N) {

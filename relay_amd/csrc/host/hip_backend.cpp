@@ -686,8 +686,17 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
         act_ready = true;
       } else {
         if (!mlp_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.mlp_norm.p, H, eps, xn_.p, stream_));
-        const int ks = I % 8 == 0 ? w8_partials(L.w_gate_up, xn_.p, T) : 0;
-        if (ks) {
+        // Above 64 tokens, where the plan runs gate_up unsplit on the 256 x 96 tile: the same
+        // product with SiLU·mul in its epilogue (same bytes, no fp32 [T, 2 I] round trip).
+        const bool tile_silu = L.w_gate_up.i8.p && T > 64 && rh_gemm_w8_plan(T, H, 2 * I) == 1 &&
+                               rh_gemm_w8_kernel(T, H, 2 * I, 1) == 1 &&
+                               (static_cast<std::int64_t>(I) + 256) * L.w_gate_up.ldw < (std::int64_t(1) << 31);
+        const int ks = tile_silu || I % 8 ? 0 : w8_partials(L.w_gate_up, xn_.p, T);
+        if (tile_silu) {
+          RH_CHECK(rh_gemm_w8_gate_up_silu(L.w_gate_up.i8.p, L.w_gate_up.ldw, L.w_gate_up.scale.p, xn_.p, act_.p, T, H,
+                                           I, stream_));
+          act_ready = true;
+        } else if (ks) {
           RH_CHECK(rh_w8_merge_silu(split_ws_.p, ks, T, I, L.w_gate_up.scale.p, act_.p, stream_));
           act_ready = true;
         } else if (i8_silu) {

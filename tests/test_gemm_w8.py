@@ -312,3 +312,55 @@ def test_merge_fused_limits(torch_mod, dev):
     assert L.rh_w8_merge_rmsnorm_fits(4096) and not L.rh_w8_merge_rmsnorm_fits(4100) and not L.rh_w8_merge_rmsnorm_fits(8192)
     assert L.rh_gemm_w8_partials(None, 128, None, 4, 128, 64, 1, None, None) != 0 and "ksplit" in _lib.last_error()
     assert L.rh_w8_merge_silu(None, 2, 4, 12, None, None, None) != 0
+
+
+@pytest.mark.parametrize("T,I,K", [(560, 14336, 4096), (512, 5632, 2048), (100, 1000, 256), (129, 250, 128),
+                                   (300, 1536, 576), (65, 130, 64), (1, 64, 64), (97, 8, 192)])
+def test_gate_up_silu_equals_the_chain(torch_mod, dev, T, I, K):
+    """rh_gemm_w8_gate_up_silu against rh_gemm_w8 into an fp32 [T, 2 I] buffer + rh_silu_mul:
+    the same bytes where the chain's product runs the same 256 x 96 tile (rh_gemm_w8_kernel
+    = 1); elsewhere within the fp32 accumulation bound of g and u carried through SiLU·mul
+    plus one fp16 rounding (checked on sampled outputs). Covers partial row and token tiles
+    and I not a multiple of 4 (scalar stores)."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    q, s, x = make(2 * I, K, T, seed=T * 7 + I + K)
+    W, S, X = dt(q), dt(s), dt(x.view(np.int16))
+    gu = torch.empty((T, 2 * I), device=dev)
+    act_a = torch.empty((T, I), dtype=torch.int16, device=dev)
+    act_b = torch.full((T, I), 0x7E00, dtype=torch.int16, device=dev)
+    print(f"gemm_w8_gate_up_silu case: T={T} I={I} K={K}", flush=True)
+    _lib.check(L.rh_gemm_w8(W.data_ptr(), K, S.data_ptr(), X.data_ptr(), gu.data_ptr(), T, K, 2 * I, 0.0, None),
+               "rh_gemm_w8")
+    _lib.check(L.rh_silu_mul(gu.data_ptr(), T, I, act_a.data_ptr(), None), "rh_silu_mul")
+    _lib.check(L.rh_gemm_w8_gate_up_silu(W.data_ptr(), K, S.data_ptr(), X.data_ptr(), act_b.data_ptr(), T, K, I, None),
+               "rh_gemm_w8_gate_up_silu")
+    torch.cuda.synchronize()
+    a, b = act_a.cpu().numpy(), act_b.cpu().numpy()
+    if L.rh_gemm_w8_kernel(T, K, 2 * I, 1) == 1:
+        assert np.array_equal(a, b)
+    rows = np.unique(np.random.default_rng(I).integers(0, I, size=min(I, 256)))
+    qd, xd, sd = q.astype(np.float64), x.astype(np.float64), s.astype(np.float64)
+    cols = np.concatenate([rows, I + rows])
+    dot = (xd @ qd[cols].T) * sd[cols]
+    err = (4 * K * EPS32 + 2 * EPS32) * (np.abs(xd) @ np.abs(qd[cols]).T) * sd[cols] + 1e-30
+    n = len(rows)
+    g, u, eg, eu = dot[:, :n], dot[:, n:], err[:, :n], err[:, n:]
+    silu = g / (1.0 + np.exp(-g))
+    tol = 1.1 * np.abs(u) * eg + np.abs(silu) * eu + eg * eu
+    want = silu * u
+    for got in (a, b):
+        v = got[:, rows].view(np.float16).astype(np.float64)
+        lim = tol + 2.0 ** -10 * np.maximum(np.abs(v), np.abs(want)) + 2.0 ** -24
+        assert (np.abs(v - want) <= lim).all()
+
+
+def test_gate_up_silu_limits(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemm_w8_gate_up_silu(None, 128, None, None, None, 4, 128, 64, None) != 0
+    assert "missing pointer" in _lib.last_error()
