@@ -710,7 +710,11 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
         }
       }
     }
-    if (fused(L.w_down, T)) {
+    // The SiLU prologue computes T x I activations in every workgroup: only while that is
+    // small (TinyLlama fp16 decode, I = 5632: b = 2 1.085 -> 1.063 ms, b = 4 1.177 -> 1.103
+    // with the separate SiLU launch, level at b = 1 and 8; SmolLM2-135M, I = 1536, b = 1
+    // fused: 1087 against 1048 tok/s).
+    if (fused(L.w_down, T) && T * I <= 8192) {
       RH_CHECK(rh_gemv_f16_silu(L.w_down.f16.p, I, gu_.p, x_.p, T, I, H, 1.0f, stream_));  // x += act W_down^T
     } else {
       if (!act_ready) RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));
