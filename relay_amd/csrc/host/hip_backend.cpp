@@ -218,7 +218,11 @@ class HipBackend final : public Backend {
   // Whether gemm_f16 runs the skinny product (else the library GEMM) for this shape.
   static bool skinny(int K, int N, int T);
   void kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in, const void* v_in);
-  static constexpr int kKvChunks = 16;                          // pieces of one KV transfer
+  // Pieces of one KV transfer: writes in up to 16, reads in up to 8 (each DMA piece costs
+  // ~10 us beyond its bytes, and a read's host copies are split over the threads; Llama-3
+  // layer reads of 33.6 MB: 34.1 GB/s at 16 pieces, 36.9-38.8 at 8, 38.5-39.1 at 4, 28-31 at 2;
+  // writes 35.5 at 16, 34-36 at 8, 30.5 at 4).
+  static constexpr int kKvChunks = 16, kKvReadChunks = 8;
   static constexpr int kKvThreads = 4;                          // host threads copying them (8: no faster)
   static constexpr std::size_t kKvMinPiece = std::size_t(1) << 20;
   std::vector<hipEvent_t> kv_events_;                           // one per piece in flight
@@ -818,10 +822,10 @@ void HipBackend::finish_forward(float* dst, std::size_t n) {
 }
 
 // KV block traffic on the copy stream: gather into a contiguous device buffer and copy it
-// to pinned host memory (and the reverse for writes), in up to kKvChunks pieces so that the
-// host-side memcpy of one piece runs under the DMA of the next (one Llama-3-8B layer at
-// 8192 positions, 33.6 MB, into and out of caller buffers: writes 20.8 -> 30.5 GB/s; reads
-// 26.4 GB/s). Serialised by copy_mu_.
+// to pinned host memory (and the reverse for writes), in pieces so that the host-side
+// memcpy of one piece runs under the DMA of the next (one Llama-3-8B layer at 8192
+// positions, 33.6 MB, into and out of caller buffers: one piece 10.9 / 20.8 GB/s read /
+// write, pieces on one host thread 26.4 / 30.5, now ~37 / ~36). Serialised by copy_mu_.
 void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, void* v_out, const void* k_in,
                        const void* v_in) {
   if (layer < 0 || layer >= c_.layers) throw std::invalid_argument("layer out of range");
@@ -844,7 +848,8 @@ void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, v
     for (auto& e : kv_events_) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
   // Staging bytes [0, n bb) are K, [n bb, 2 n bb) V; piece i covers [i piece, (i+1) piece).
-  const std::size_t piece = std::max<std::size_t>(kKvMinPiece, (bytes + kKvChunks - 1) / kKvChunks);
+  const int chunks = k_out ? kKvReadChunks : kKvChunks;
+  const std::size_t piece = std::max<std::size_t>(kKvMinPiece, (bytes + chunks - 1) / chunks);
   const int pieces = static_cast<int>((bytes + piece - 1) / piece);
   // The host-side copies between the caller's buffers and the pinned staging run on a few
   // threads (one core moves ~10-25 GB/s; the DMA runs at the PCIe rate).
@@ -870,10 +875,14 @@ void HipBackend::kv_io(int layer, const std::vector<int>& blocks, void* k_out, v
       HIP_CHECK(hipMemcpyAsync(host + a, kv_stage_dev_.p + a, len, hipMemcpyDeviceToHost, copy_stream_));
       HIP_CHECK(hipEventRecord(kv_events_[i], copy_stream_));
     }
+    // Every thread copies its share of every piece as the piece lands, so the copy after
+    // the last DMA is a share of one piece, not a whole piece on one thread.
     run_shares(workers, [&](int j) {
-      for (int i = j; i < pieces; i += workers) {
+      for (int i = 0; i < pieces; ++i) {
         HIP_CHECK(hipEventSynchronize(kv_events_[i]));
-        user_copy(i * piece, std::min(piece, bytes - i * piece), true);
+        const std::size_t a = i * piece, len = std::min(piece, bytes - a);
+        auto cut = [&](int k) { return k == workers ? len : std::min(len, (len * k / workers + 4095) & ~std::size_t(4095)); };
+        user_copy(a + cut(j), cut(j + 1) - cut(j), true);
       }
     });
   } else {
