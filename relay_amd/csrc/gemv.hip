@@ -866,7 +866,9 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 // (kRmsNorm, stage_operands: rows K + 8 halves apart, so the 16 lanes of a B read cover 8
 // tokens x 2 halves on distinct banks). One writer thread per (token, row) sums the waves'
 // partials in a fixed order; kRope writers take a pair (m, m + 8) and apply qkv_post's
-// arithmetic (rope_epilogue's float operations).
+// arithmetic (rope_epilogue's float operations). kSilu: W is the fused [gate; up] matrix and
+// the workgroup's two 8-row groups are gate rows a0 + 4 rt .. +3 and the up rows I further
+// (a0 = 8 blockIdx.x), so it writes act = fp16(silu(g) * u) for 8 outputs (fp16 [T, I]).
 template <int WAVES, int DEPTH, bool F16_SCALE, int PRO, int EPI>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     const int8_t* __restrict__ w8, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
