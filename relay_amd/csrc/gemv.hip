@@ -869,12 +869,17 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 // arithmetic (rope_epilogue's float operations). kSilu: W is the fused [gate; up] matrix and
 // the workgroup's two 8-row groups are gate rows a0 + 4 rt .. +3 and the up rows I further
 // (a0 = 8 blockIdx.x), so it writes act = fp16(silu(g) * u) for 8 outputs (fp16 [T, I]).
-template <int WAVES, int DEPTH, bool F16_SCALE, int PRO, int EPI>
+// W16: fp16 weights (gemv_f16_m8_kernel's layout: a step is 64 k, lane (c, g) loads the 8
+// halves at k + 32 (c % 2) + 8 g, one MFMA per step and row group, no scale); a row's step
+// is 128 bytes either way, so the weight addressing is shared.
+template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
-    const int8_t* __restrict__ w8, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
+    const void* __restrict__ wq, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
     const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
-  static_assert(PRO == kPlain || PRO == kRmsNorm, "the whole-line fused form takes RMSNorm or no producer");
-  constexpr int RT = 2;
+  static_assert(!W16 || EPI != kSilu, "the SiLU epilogue is the int8 form's");
+  constexpr int RT = 2, KS = W16 ? 64 : 128;  // k per step
+  const int8_t* w8 = static_cast<const int8_t*>(wq);
+  const int64_t ldb = W16 ? 2 * ldw : ldw;  // row stride in bytes
   __shared__ float red[WAVES][8][8 * RT];
   __shared__ float s_inv[8];
   __shared__ int s_pos[EPI == kRope ? 8 : 1];
@@ -888,21 +893,22 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     if (EPI == kSilu) return min(a0 + 4 * rt + (m & 3), I - 1) + (m >= 4 ? I : 0);
     return EPI == kRope ? rope_tile_row(blockIdx.x, 8 * rt + m, ra.D) : 16 * blockIdx.x + 8 * rt + m;
   };
-  const int nsteps = (K + 127) / 128;
+  const int nsteps = (K + KS - 1) / KS;
   const int per = (nsteps + WAVES - 1) / WAVES;
   const int s0 = w * per, s1 = min(nsteps, s0 + per);
-  const int8_t* wr[RT];
+  const int klane = W16 ? 32 * h + 8 * g : 64 * h + 16 * g;  // this lane's first k of a step
+  const int8_t* wr[RT];  // byte addresses; a step is 128 bytes of a row for both weight types
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
-    wr[rt] = w8 + static_cast<int64_t>(min(out_row(rt, r), N - 1)) * ldw + 64 * h + 16 * g;
+    wr[rt] = w8 + static_cast<int64_t>(min(out_row(rt, r), N - 1)) * ldb + 64 * h + 16 * g;
   const bool tok = r < T;
-  const half_t* xr = static_cast<const half_t*>(xin) + static_cast<int64_t>(tok ? r : 0) * K + 64 * h + 16 * g;
+  const half_t* xr = static_cast<const half_t*>(xin) + static_cast<int64_t>(tok ? r : 0) * K + klane;
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   uint4v wv[DEPTH][RT];
   auto load_w = [&](int st) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int k = (st + d) * 128 + 64 * h + 16 * g;
+      const int k = (st + d) * KS + klane;
       const bool live = st + d < s1 && k < K;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
@@ -910,7 +916,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     }
   };
   load_w(s0);  // the first weights are in flight under the prologue
-  if (PRO == kRmsNorm) stage_operands<PRO, WAVES, WAVES >= 16 ? 4 : 8>(xin, norm_w, eps, T, K, sxb, s_inv);
+  if (PRO != kPlain) stage_operands<PRO, WAVES, WAVES >= 16 ? 4 : 8>(xin, norm_w, eps, T, K, sxb, s_inv);
   if (EPI == kRope && w == WAVES - 1) rope_lookups(ra, blockIdx.x, T, lane, s_pos, s_kvrow);
   float4v acc[RT];
 #pragma unroll
@@ -920,23 +926,27 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     half8 xa[DEPTH], xb[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int k = (st + d) * 128 + 64 * h + 16 * g;
+      const int k = (st + d) * KS + klane;
       const bool live = st + d < s1 && k < K;
       if (PRO == kPlain) {
-        xa[d] = live && tok ? load_half8(xr + (st + d) * 128) : zero;
-        xb[d] = live && tok ? load_half8(xr + (st + d) * 128 + 8) : zero;
+        xa[d] = live && tok ? load_half8(xr + (st + d) * KS) : zero;
+        if (!W16) xb[d] = live && tok ? load_half8(xr + (st + d) * KS + 8) : zero;
       } else {
         const half_t* xs = sxb + (tok ? r : 0) * (K + 8) + k;
         xa[d] = live && tok ? *reinterpret_cast<const half8*>(xs) : zero;
-        xb[d] = live && tok ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+        if (!W16) xb[d] = live && tok ? *reinterpret_cast<const half8*>(xs + 8) : zero;
       }
     }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]), xa[d], acc[rt]);
-        acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]), xb[d], acc[rt]);
+        if (W16) {
+          acc[rt] = mfma16x16x32(__builtin_bit_cast(half8, wv[d][rt]), xa[d], acc[rt]);
+        } else {
+          acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]), xa[d], acc[rt]);
+          acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]), xb[d], acc[rt]);
+        }
       }
   }
   // Lane (column 2t + h, g) holds C rows 4g + q = (row 2g + q / 2, half q % 2).
@@ -958,7 +968,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     float v = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < WAVES; ++ww) v += red[ww][t][m];
-    return v * row_scale(min(out_row(m >> 3, m & 7), N - 1));
+    return W16 ? v : v * row_scale(min(out_row(m >> 3, m & 7), N - 1));
   };
   if constexpr (EPI == kStore) {
     const int t = threadIdx.x / 16, m = threadIdx.x % 16;
@@ -1027,11 +1037,11 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
   if constexpr (PRO != kSiluMul) {
     if (T <= 8) {
       if (tiles < 256) {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, F16_SCALE, PRO, EPI>), dim3(tiles),
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, false, F16_SCALE, PRO, EPI>), dim3(tiles),
                                          dim3(16 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
                                          beta, ra));
       } else {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, F16_SCALE, PRO, EPI>), dim3(tiles),
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, false, F16_SCALE, PRO, EPI>), dim3(tiles),
                                          dim3(8 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
                                          beta, ra));
       }
@@ -1095,11 +1105,11 @@ int launch_m8_rmsnorm_silu(const int8_t* w8, int64_t ldw, const void* scale, con
   const int tiles = (I + 7) / 8, N = 2 * I;
   float* out = reinterpret_cast<float*>(act);
   if (tiles < 256) {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, false, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
                                      dim3(16 * kWave), staged, s, w8, ldw, scale, x, norm_w, eps, out, T, K, N, 0.0f,
                                      RopeArgs{}));
   } else {
-    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
+    RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, false, F16_SCALE, kRmsNorm, kSilu>), dim3(tiles),
                                      dim3(8 * kWave), staged, s, w8, ldw, scale, x, norm_w, eps, out, T, K, N, 0.0f,
                                      RopeArgs{}));
   }
@@ -1395,6 +1405,22 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
     return launch_f16_t1(wt, ldw, static_cast<const half_t*>(x), y, K, N, beta, s);
   if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_m8_takes(T))
     return launch_f16_m8(wt, ldw, static_cast<const half_t*>(x), y, T, K, N, beta, s);
+  if constexpr (PRO != kPlain || EPI != kStore) {
+    if (ksplit == 1 && T <= 8) {
+      // A producer or the qkv epilogue at 1-8 tokens: the whole-line fused kernel (16 rows
+      // per workgroup, K split over the waves in 64-k steps).
+      if (tiles < 256) {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 4, true, false, PRO, EPI>), dim3(tiles),
+                                         dim3(16 * kWave), staged, s, wt, ldw, nullptr, x, norm_w, eps, y, T, K, N,
+                                         beta, ra));
+      } else {
+        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 4, true, false, PRO, EPI>), dim3(tiles),
+                                         dim3(8 * kWave), staged, s, wt, ldw, nullptr, x, norm_w, eps, y, T, K, N,
+                                         beta, ra));
+      }
+      return 0;
+    }
+  }
   if (T <= kMaxTokens) {
     if (wide) {
       RH_GEMV_F16(16, 1);
