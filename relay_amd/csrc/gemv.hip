@@ -1339,13 +1339,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_f16_m8_kernel(const half_t
   }
 }
 
-// Plain fp16 products at 2-8 tokens take gemv_f16_m8_kernel: 8 waves of 4 steps, 4 waves of 8
+// Plain fp16 products at 1-8 tokens (one token: below 2 Mi weights) take gemv_f16_m8_kernel: 8 waves of 4 steps, 4 waves of 8
 // below 256 workgroups. Measured (us, 16-row tile -> this, T = 2 / 4 / 8): TinyLlama 2048 x
 // 2048 5.8 / 6.0 / 6.2 -> 3.9 / 4.1 / 3.8, 2048 -> 11264 14.3 / 14.8 / 14.7 -> 9.2 / 9.4 /
 // 10.6, 5632 -> 2048 9.8 / 10.1 / 11.2 -> 6.3 / 6.3 / 6.6; 4096 -> 14336 24.2 / 25.8 / 28.6
 // -> 20.9 / 20.8 / 23.3; SmolLM2 1536 -> 576 4.5 / 4.6 / 4.9 -> 3.9 / 4.1 / 4.0, 576 -> 960
-// level (~4.0, latency).
-bool f16_m8_takes(int T) { return T >= 2 && T <= 8; }
+// level (~4.0, latency). One token too below gemv_f16_t1_kernel's range (SmolLM2-135M fp16
+// decode step 0.816 -> 0.800 ms; on the t1 kernel's matrices the two were level).
+bool f16_m8_takes(int T) { return T >= 1 && T <= 8; }
 
 int launch_f16_m8(const half_t* wt, int64_t ldw, const half_t* x, float* y, int T, int K, int N, float beta,
                   hipStream_t s) {

@@ -19,9 +19,8 @@ EPS32 = 2.0 ** -24
 
 def whole_line(T, N, K):
     """Whether rh_gemv_f16 takes a whole-line kernel (the vector-ALU one at one token from 2 Mi
-    weights, the 8-row MFMA one at 2-8 tokens) instead of the 16-row MFMA tile that the fused
-    launches use: then the two sum in different orders."""
-    return (T == 1 and N * K >= 1 << 21) or 2 <= T <= 8
+    weights, the 8-row MFMA one at 1-8 tokens otherwise) instead of the 16-row MFMA tile."""
+    return 1 <= T <= 8
 
 
 def fused_differs(T, N, K):
@@ -94,10 +93,11 @@ def test_one_token_kernel(torch_mod, dev, N, K, ldw):
 
 
 @pytest.mark.parametrize("N,K,T,ldw", [(11264, 2048, 8, 2048), (576, 1536, 3, 1544), (2048, 5632, 2, 5632),
-                                       (13, 4112, 7, 4120)])
+                                       (13, 4112, 7, 4120), (576, 576, 1, 584), (960, 576, 1, 576), (21, 1000 * 16, 1, 16008)])
 def test_few_token_kernel(torch_mod, dev, N, K, T, ldw):
-    """2-8 tokens on the 8-row whole-line MFMA kernel (8 waves; 4 below 256 workgroups), padded
-    rows, a K that ends mid-step, a last workgroup with five rows, beta = 1 over a finite y."""
+    """1-8 tokens (one token below 2 Mi weights) on the 8-row whole-line MFMA kernel (8 waves;
+    4 below 256 workgroups), padded rows, a K that ends mid-step, a last workgroup with five
+    rows, beta = 1 over a finite y."""
     w, x = make(N, K, T, seed=N + K + T)
     y0 = np.random.default_rng(K).standard_normal((T, N)).astype(np.float32)
     check(run(torch_mod, dev, w, x, beta=1.0, y0=y0, ldw=ldw), w, x, beta=1.0, y0=y0)
