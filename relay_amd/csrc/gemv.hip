@@ -872,12 +872,15 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 // W16: fp16 weights (gemv_f16_m8_kernel's layout: a step is 64 k, lane (c, g) loads the 8
 // halves at k + 32 (c % 2) + 8 g, one MFMA per step and row group, no scale); a row's step
 // is 128 bytes either way, so the weight addressing is shared.
-template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI>
+// RT = 1 (kStore only): one 8-row group per workgroup, for matrices whose 16-row tiles would
+// leave CUs idle.
+template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI, int RT = 2>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     const void* __restrict__ wq, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
     const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
   static_assert(!W16 || EPI != kSilu, "the SiLU epilogue is the int8 form's");
-  constexpr int RT = 2, KS = W16 ? 64 : 128;  // k per step
+  static_assert(RT == 2 || (RT == 1 && EPI == kStore), "the qkv and SiLU epilogues pair rows in 16-row tiles");
+  constexpr int KS = W16 ? 64 : 128;  // k per step
   const int8_t* w8 = static_cast<const int8_t*>(wq);
   const int64_t ldb = W16 ? 2 * ldw : ldw;  // row stride in bytes
   __shared__ float red[WAVES][8][8 * RT];
@@ -891,7 +894,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
   const int I = N / 2, a0 = 8 * blockIdx.x;  // kSilu only
   auto out_row = [&](int rt, int m) -> int {  // m < 8: row m of group rt
     if (EPI == kSilu) return min(a0 + 4 * rt + (m & 3), I - 1) + (m >= 4 ? I : 0);
-    return EPI == kRope ? rope_tile_row(blockIdx.x, 8 * rt + m, ra.D) : 16 * blockIdx.x + 8 * rt + m;
+    return EPI == kRope ? rope_tile_row(blockIdx.x, 8 * rt + m, ra.D) : 8 * RT * blockIdx.x + 8 * rt + m;
   };
   const int nsteps = (K + KS - 1) / KS;
   const int per = (nsteps + WAVES - 1) / WAVES;
@@ -971,9 +974,9 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     return W16 ? v : v * row_scale(min(out_row(m >> 3, m & 7), N - 1));
   };
   if constexpr (EPI == kStore) {
-    const int t = threadIdx.x / 16, m = threadIdx.x % 16;
-    const int n = 16 * blockIdx.x + m;
-    if (threadIdx.x < 16 * T && n < N) {
+    const int t = threadIdx.x / (8 * RT), m = threadIdx.x % (8 * RT);
+    const int n = 8 * RT * blockIdx.x + m;
+    if (threadIdx.x < 8 * RT * T && n < N) {
       float* dst = y + static_cast<int64_t>(t) * N + n;
       *dst = value(t, m) + (beta != 0.0f ? beta * *dst : 0.0f);
     }
@@ -1409,7 +1412,16 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
   if constexpr (PRO != kPlain || EPI != kStore) {
     if (ksplit == 1 && T <= 8) {
       // A producer or the qkv epilogue at 1-8 tokens: the whole-line fused kernel (16 rows
-      // per workgroup, K split over the waves in 64-k steps).
+      // per workgroup, 8 where that still leaves <= 256 workgroups and no row pairing is
+      // needed; K split over the waves in 64-k steps).
+      if constexpr (EPI == kStore) {
+        if ((N + 7) / 8 <= 256) {
+          RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 4, true, false, PRO, EPI, 1>),
+                                           dim3((N + 7) / 8), dim3(16 * kWave), staged, s, wt, ldw, nullptr, x, norm_w,
+                                           eps, y, T, K, N, beta, ra));
+          return 0;
+        }
+      }
       if (tiles < 256) {
         RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 4, true, false, PRO, EPI>), dim3(tiles),
                                          dim3(16 * kWave), staged, s, wt, ldw, nullptr, x, norm_w, eps, y, T, K, N,
