@@ -168,11 +168,10 @@ int rh_gemv_int8_max_tokens(void);
  * launches around the GEMV, cuda_backend.cu:575-591): the int8 counterparts of
  * rh_gemv_f16_rmsnorm, rh_gemv_f16_silu, rh_gemv_f16_qkv and rh_gemv_f16_rmsnorm_qkv, with
  * their operands and limits (rh_gemv_f16_fused_fits(T, K) for the fused producers) and
- * rh_gemv_int8's weights and scales. At 9-16 tokens each gives the bits of the launches it
- * replaces (both run the 16-row tile); at 1-8 tokens the plain rh_gemv_int8 and the RMSNorm
- * and qkv forms run whole-line kernels that split K over a different number of waves, and
- * rh_gemv_int8_silu runs the 16-row tile, so there the fused results agree with the
- * launches they replace within the fp32 accumulation bound 4 * K * 2^-24 * sum|w * x|. */
+ * rh_gemv_int8's weights and scales. At 1-16 tokens the plain rh_gemv_int8 and the RMSNorm
+ * and qkv forms run whole-line kernels whose row groups and wave splits can differ, and
+ * rh_gemv_int8_silu runs the 16-row tile, so the fused results agree with the launches they
+ * replace within the fp32 accumulation bound 4 * K * 2^-24 * sum|w * x|. */
 int rh_gemv_int8_rmsnorm(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* x,
                          const float* norm_w, float eps, float* y, int T, int K, int N, float beta, void* stream);
 int rh_gemv_int8_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const float* gu, float* y,
@@ -234,9 +233,10 @@ int rh_gemv_f16_split_plan(int T, int K, int N);
  *             sum of squares in double (rh_rmsnorm's arithmetic);
  *   _silu:    gu fp32 [T, 2K] (gate | up) -> fp16(g / (1 + exp(-g)) * u) (rh_silu_mul's).
  * Requires rh_gemv_f16_fused_fits(T, K) (T * (K + 8) fp16 values fit 64 KB of LDS).
- * At 1-8 tokens these (and rh_gemv_f16_qkv / _rmsnorm_qkv) run a whole-line kernel that
- * splits K differently from rh_gemv_f16, so they agree with the two-launch chain within the
- * fp32 accumulation bound; at 9-32 tokens, where both take the 16-row tile, bit for bit. */
+ * At 1-16 tokens these (and rh_gemv_f16_qkv / _rmsnorm_qkv) run a whole-line kernel whose
+ * row groups and wave split can differ from rh_gemv_f16's, so they agree with the two-launch
+ * chain within the fp32 accumulation bound; at 17-32 tokens, where both take the 16-row
+ * tile, bit for bit. */
 int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps, float* y,
                         int T, int K, int N, float beta, void* stream);
 int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N, float beta,

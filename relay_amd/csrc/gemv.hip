@@ -794,9 +794,16 @@ int launch_m8_silu(const int8_t* w8, int64_t ldw, const void* scale, const half_
   return 0;
 }
 
+template <bool W16, bool F16_SCALE, int PRO, int EPI>
+int launch_whole_line(const void* w, int64_t ldw, const void* scale, const void* x, const float* norm_w, float eps,
+                      float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra);
+
 template <bool F16_SCALE>
 int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, float* y, int T, int K, int N,
            float beta, hipStream_t s) {
+  if (T >= 9 && T <= 16 && N <= 6144)  // 9-16 tokens on up to 6144 rows: the whole-line kernel
+    return launch_whole_line<false, F16_SCALE, kPlain, kStore>(w8, ldw, scale, x, nullptr, 0.0f, y, T, K, N, beta, s,
+                                                                RopeArgs{});
   if (m8_takes(T, K, N)) {
     if (m8_one_round(N)) {
       RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_kernel<16, 1, F16_SCALE>), dim3((N + 7) / 8), dim3(16 * kWave), 0,
@@ -874,7 +881,7 @@ int launch(const int8_t* w8, int64_t ldw, const void* scale, const half_t* x, fl
 // is 128 bytes either way, so the weight addressing is shared.
 // RT = 1 (kStore only): one 8-row group per workgroup, for matrices whose 16-row tiles would
 // leave CUs idle.
-template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI, int RT = 2>
+template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI, int RT = 2, int NB = 1>
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     const void* __restrict__ wq, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
     const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
@@ -883,14 +890,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
   constexpr int KS = W16 ? 64 : 128;  // k per step
   const int8_t* w8 = static_cast<const int8_t*>(wq);
   const int64_t ldb = W16 ? 2 * ldw : ldw;  // row stride in bytes
-  __shared__ float red[WAVES][8][8 * RT];
-  __shared__ float s_inv[8];
-  __shared__ int s_pos[EPI == kRope ? 8 : 1];
-  __shared__ int64_t s_kvrow[EPI == kRope ? 8 : 1];
+  __shared__ float red[WAVES][8 * NB][8 * RT];
+  __shared__ float s_inv[8 * NB];
+  __shared__ int s_pos[EPI == kRope ? 8 * NB : 1];
+  __shared__ int64_t s_kvrow[EPI == kRope ? 8 * NB : 1];
   extern __shared__ __attribute__((aligned(16))) half_t sxb[];  // kRmsNorm: [T][K + 8]
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int r = c >> 1, h = c & 1;  // A row: row r of group rt, half h; B column: token r, half h
+  const int r = c >> 1, h = c & 1;  // A row: row r of group rt, half h; B column: token r (+ 8 nb), half h
   const int I = N / 2, a0 = 8 * blockIdx.x;  // kSilu only
   auto out_row = [&](int rt, int m) -> int {  // m < 8: row m of group rt
     if (EPI == kSilu) return min(a0 + 4 * rt + (m & 3), I - 1) + (m >= 4 ? I : 0);
@@ -904,8 +911,13 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
     wr[rt] = w8 + static_cast<int64_t>(min(out_row(rt, r), N - 1)) * ldb + 64 * h + 16 * g;
-  const bool tok = r < T;
-  const half_t* xr = static_cast<const half_t*>(xin) + static_cast<int64_t>(tok ? r : 0) * K + klane;
+  bool tok[NB];
+  const half_t* xr[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    tok[nb] = r + 8 * nb < T;
+    xr[nb] = static_cast<const half_t*>(xin) + static_cast<int64_t>(tok[nb] ? r + 8 * nb : 0) * K + klane;
+  }
   const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   uint4v wv[DEPTH][RT];
   auto load_w = [&](int st) {
@@ -921,23 +933,28 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
   load_w(s0);  // the first weights are in flight under the prologue
   if (PRO != kPlain) stage_operands<PRO, WAVES, WAVES >= 16 ? 4 : 8>(xin, norm_w, eps, T, K, sxb, s_inv);
   if (EPI == kRope && w == WAVES - 1) rope_lookups(ra, blockIdx.x, T, lane, s_pos, s_kvrow);
-  float4v acc[RT];
+  float4v acc[RT][NB];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[rt][nb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
   for (int st = s0; st < s1; st += DEPTH) {
     if (st != s0) load_w(st);
-    half8 xa[DEPTH], xb[DEPTH];
+    half8 xa[DEPTH][NB], xb[DEPTH][NB];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int k = (st + d) * KS + klane;
       const bool live = st + d < s1 && k < K;
-      if (PRO == kPlain) {
-        xa[d] = live && tok ? load_half8(xr + (st + d) * KS) : zero;
-        if (!W16) xb[d] = live && tok ? load_half8(xr + (st + d) * KS + 8) : zero;
-      } else {
-        const half_t* xs = sxb + (tok ? r : 0) * (K + 8) + k;
-        xa[d] = live && tok ? *reinterpret_cast<const half8*>(xs) : zero;
-        if (!W16) xb[d] = live && tok ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (PRO == kPlain) {
+          xa[d][nb] = live && tok[nb] ? load_half8(xr[nb] + (st + d) * KS) : zero;
+          if (!W16) xb[d][nb] = live && tok[nb] ? load_half8(xr[nb] + (st + d) * KS + 8) : zero;
+        } else {
+          const half_t* xs = sxb + (tok[nb] ? r + 8 * nb : 0) * (K + 8) + k;
+          xa[d][nb] = live && tok[nb] ? *reinterpret_cast<const half8*>(xs) : zero;
+          if (!W16) xb[d][nb] = live && tok[nb] ? *reinterpret_cast<const half8*>(xs + 8) : zero;
+        }
       }
     }
 #pragma unroll
@@ -945,23 +962,32 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         if (W16) {
-          acc[rt] = mfma16x16x32(__builtin_bit_cast(half8, wv[d][rt]), xa[d], acc[rt]);
+          const half8 a = __builtin_bit_cast(half8, wv[d][rt]);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[rt][nb] = mfma16x16x32(a, xa[d][nb], acc[rt][nb]);
         } else {
-          acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]), xa[d], acc[rt]);
-          acc[rt] = mfma16x16x32(int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]), xb[d], acc[rt]);
+          const half8 a = int8x8_to_half8(wv[d][rt][0], wv[d][rt][1]);
+          const half8 b = int8x8_to_half8(wv[d][rt][2], wv[d][rt][3]);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            acc[rt][nb] = mfma16x16x32(a, xa[d][nb], acc[rt][nb]);
+            acc[rt][nb] = mfma16x16x32(b, xb[d][nb], acc[rt][nb]);
+          }
         }
       }
   }
   // Lane (column 2t + h, g) holds C rows 4g + q = (row 2g + q / 2, half q % 2).
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float m0 = h ? acc[rt][1] : acc[rt][0], m1 = h ? acc[rt][3] : acc[rt][2];
-    const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
-    if (h == 0 && tok) {
-      red[w][r][8 * rt + 2 * g] = v0;
-      red[w][r][8 * rt + 2 * g + 1] = v1;
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float m0 = h ? acc[rt][nb][1] : acc[rt][nb][0], m1 = h ? acc[rt][nb][3] : acc[rt][nb][2];
+      const float v0 = m0 + __shfl_xor(m0, 1), v1 = m1 + __shfl_xor(m1, 1);
+      if (h == 0 && tok[nb]) {
+        red[w][r + 8 * nb][8 * rt + 2 * g] = v0;
+        red[w][r + 8 * nb][8 * rt + 2 * g + 1] = v1;
+      }
     }
-  }
   __syncthreads();
   auto row_scale = [&](int n) {
     return F16_SCALE ? static_cast<float>(static_cast<const half_t*>(scale)[n]) : static_cast<const float*>(scale)[n];
@@ -1025,31 +1051,63 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
   }
 }
 
-// The int8 product with a fused producer (PRO) and/or the qkv epilogue (EPI): 16-row
-// workgroups with the wave count of the 16-row tile's plain launch for the same N, so at
-// 9-16 tokens the sums are the plain product's bit for bit; at 1-8 tokens the plain product
-// runs the whole-line kernel (another summation order: equal within the fp32 bound).
+// The whole-line kernel at 1-16 tokens (two 8-token column blocks above 8): 8-row workgroups
+// for plain stores while they fit one round on the CUs, else 16-row ones (row pairs for
+// the qkv and SiLU epilogues); 16 waves below 256 workgroups, else 8. Measured at 9-16 tokens
+// against the 16-row MFMA tile (us, T = 9 / 16): fp16 2048 x 2048 6.2 / 6.5 -> 4.6 / 4.8,
+// 5632 -> 2048 11.3 / 13.0 -> 7.9 / 8.8, 2048 -> 11264 15.2 / 17.1 -> 13.2 / 13.6, 4096 ->
+// 14336 29.8 / 34.7 -> 25.7 / 27.2, 14336 -> 4096 30.0 / 30.7 -> 25.1 / 25.8; int8 2048 x 2048
+// 5.4 / 5.9 -> 4.7 / 5.1, 5632 -> 2048 9.4 / 11.0 -> 7.1 / 9.2, 2048 -> 2560 5.6 / 5.9 -> 4.8 /
+// 5.4, 4096 x 4096 8.1 / 9.0 -> 7.5 / 8.6, 14336 -> 4096 19.9 / 23.6 -> 19.9 / 21.7 (int8 on
+// 8192+ rows stays on its row-tile kernels: 4096 -> 14336 19.6 against 24.5 at T = 16).
+template <bool W16, bool F16_SCALE, int PRO, int EPI>
+int launch_whole_line(const void* w, int64_t ldw, const void* scale, const void* x, const float* norm_w, float eps,
+                      float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
+  const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
+  RH_REQUIRE(staged <= kFusedLdsBytes, "gemv: T * (K + 8) fp16 activations exceed the fused path's LDS");
+  RH_REQUIRE(T >= 1 && T <= 16, "gemv: the whole-line kernel takes 1-16 tokens");
+  const bool rt1 = EPI == kStore && (N + 7) / 8 <= 256;
+  const int groups = rt1 ? (N + 7) / 8 : (N + 15) / 16;
+  const bool w16 = rt1 || groups < 256;
+#define RH_WL(WAVES, DEPTH, RTV, NBV)                                                                                  \
+  RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<WAVES, DEPTH, W16, F16_SCALE, PRO, EPI, RTV, NBV>),      \
+                                   dim3(groups), dim3(WAVES * kWave), staged, s, w, ldw, scale, x, norm_w, eps, y, T, K, \
+                                   N, beta, ra))
+#define RH_WL_NB(RTV, NBV)                   \
+  if (w16) {                                 \
+    if (W16) RH_WL(16, 4, RTV, NBV);         \
+    else RH_WL(16, 1, RTV, NBV);             \
+  } else {                                   \
+    if (W16) RH_WL(8, 4, RTV, NBV);          \
+    else RH_WL(8, 2, RTV, NBV);              \
+  }
+  if constexpr (EPI == kStore) {
+    if (rt1) {
+      if (T <= 8) { RH_WL_NB(1, 1) } else { RH_WL_NB(1, 2) }
+      return 0;
+    }
+  }
+  if (T <= 8) { RH_WL_NB(2, 1) } else { RH_WL_NB(2, 2) }
+#undef RH_WL_NB
+#undef RH_WL
+  return 0;
+}
+
+// The int8 product with a fused producer (PRO) and/or the qkv epilogue (EPI): the whole-line
+// kernel at 1-16 tokens (launch_whole_line; the SiLU producer keeps the 16-row tile), the
+// 16-row tile above. Where the plain product takes another kernel or row grouping the sums
+// come in another order (equal within the fp32 bound).
 template <bool F16_SCALE, int PRO, int EPI>
 int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* xin, const float* norm_w, float eps,
                  float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
   const int tiles = (N + 15) / 16;
-  // 1-8 tokens without the SiLU producer: the whole-line form (a one-token vector-ALU form
+  // 1-16 tokens without the SiLU producer: the whole-line form (a one-token vector-ALU form
   // behind the producers made TinyLlama int8 decode steps slower).
   if constexpr (PRO != kSiluMul) {
-    if (T <= 8) {
-      if (tiles < 256) {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 1, false, F16_SCALE, PRO, EPI>), dim3(tiles),
-                                         dim3(16 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
-                                         beta, ra));
-      } else {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 2, false, F16_SCALE, PRO, EPI>), dim3(tiles),
-                                         dim3(8 * kWave), staged, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N,
-                                         beta, ra));
-      }
-      return 0;
-    }
+    if (T <= 16)
+      return launch_whole_line<false, F16_SCALE, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra);
   }
   if constexpr (PRO == kPlain) {
     if (T > kMaxTokens) {  // the qkv epilogue alone, 17-32 tokens: two column blocks
@@ -1409,30 +1467,12 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
     return launch_f16_t1(wt, ldw, static_cast<const half_t*>(x), y, K, N, beta, s);
   if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_m8_takes(T))
     return launch_f16_m8(wt, ldw, static_cast<const half_t*>(x), y, T, K, N, beta, s);
+  if (PRO == kPlain && EPI == kStore && ksplit == 1 && T >= 9 && T <= 16)
+    return launch_whole_line<true, false, kPlain, kStore>(wt, ldw, nullptr, x, nullptr, 0.0f, y, T, K, N, beta, s, ra);
   if constexpr (PRO != kPlain || EPI != kStore) {
-    if (ksplit == 1 && T <= 8) {
-      // A producer or the qkv epilogue at 1-8 tokens: the whole-line fused kernel (16 rows
-      // per workgroup, 8 where that still leaves <= 256 workgroups and no row pairing is
-      // needed; K split over the waves in 64-k steps).
-      if constexpr (EPI == kStore) {
-        if ((N + 7) / 8 <= 256) {
-          RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 4, true, false, PRO, EPI, 1>),
-                                           dim3((N + 7) / 8), dim3(16 * kWave), staged, s, wt, ldw, nullptr, x, norm_w,
-                                           eps, y, T, K, N, beta, ra));
-          return 0;
-        }
-      }
-      if (tiles < 256) {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<16, 4, true, false, PRO, EPI>), dim3(tiles),
-                                         dim3(16 * kWave), staged, s, wt, ldw, nullptr, x, norm_w, eps, y, T, K, N,
-                                         beta, ra));
-      } else {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<8, 4, true, false, PRO, EPI>), dim3(tiles),
-                                         dim3(8 * kWave), staged, s, wt, ldw, nullptr, x, norm_w, eps, y, T, K, N,
-                                         beta, ra));
-      }
-      return 0;
-    }
+    // A producer or the qkv epilogue at 1-16 tokens: the whole-line fused kernel.
+    if (ksplit == 1 && T <= 16)
+      return launch_whole_line<true, false, PRO, EPI>(wt, ldw, nullptr, x, norm_w, eps, y, T, K, N, beta, s, ra);
   }
   if (T <= kMaxTokens) {
     if (wide) {
@@ -1459,8 +1499,10 @@ extern "C" int rh_gemv_f16_split_plan(int T, int K, int N) {
   // Measured on MI355X (T = 1-32): the merge costs ~3 us (stores, counter, loads), so only
   // a long K on few row tiles gains (N = 2048, K = 5632, T = 32: 18.5 -> 14.4 us); ranges of
   // K on wider grids, or more than two, were slower everywhere.
+  // Up to 16 tokens the whole-line kernel (8-row workgroups on such matrices) is faster
+  // unsplit (5632 -> 2048 at T = 16: 8.8 us).
   const int tiles = (N + 15) / 16, nchunks = (K + kChunk - 1) / kChunk;
-  return tiles <= 128 && nchunks >= 64 ? 2 : 1;
+  return T > 16 && tiles <= 128 && nchunks >= 64 ? 2 : 1;
 }
 
 extern "C" int rh_gemv_f16_splitk(const void* w16, int64_t ldw, const void* x, float* y, int T, int K, int N,

@@ -19,15 +19,16 @@ EPS32 = 2.0 ** -24
 
 def whole_line(T, N, K):
     """Whether rh_gemv_f16 takes a whole-line kernel (the vector-ALU one at one token from 2 Mi
-    weights, the 8-row MFMA one at 1-8 tokens otherwise) instead of the 16-row MFMA tile."""
-    return 1 <= T <= 8
+    weights, the 8-row MFMA one at 1-8 tokens otherwise, the fused kernel's at 9-16) instead
+    of the 16-row MFMA tile."""
+    return 1 <= T <= 16
 
 
 def fused_differs(T, N, K):
     """Whether a fused launch (producer or qkv epilogue) and the plain launch of the chain it
-    replaces sum in different orders: at 1-8 tokens the fused forms run the 16-row
-    whole-line kernel, and above that whenever the plain launch takes a whole-line kernel."""
-    return T <= 8 or whole_line(T, N, K)
+    replaces may sum in different orders: at 1-16 tokens both run whole-line kernels, whose
+    row groups and wave splits can differ; above that both take the 16-row tile."""
+    return whole_line(T, N, K)
 
 
 def gemv_bound(w_f16, x_f16):

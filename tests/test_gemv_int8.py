@@ -21,9 +21,11 @@ EPS32 = 2.0 ** -24
 
 
 def vector_alu(T, N, K):
-    """Whether rh_gemv_int8 takes the whole-line MFMA kernel (1-8 tokens; 8 or 16 rows per
-    workgroup) instead of the 16-row MFMA tile that the fused launches use."""
-    return 1 <= T <= 8
+    """Whether a fused int8 launch and the plain launch of the chain it replaces may sum in
+    different orders: both run whole-line MFMA kernels at 1-16 tokens (8 or 16 rows per
+    workgroup, their own wave splits; rh_gemv_int8 keeps its row-tile kernels on more than
+    6144 rows at 9-16)."""
+    return 1 <= T <= 16
 
 
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):

@@ -144,7 +144,7 @@ def test_work_planners_follow_their_rules():
     """The host-side planners (no device needed): rh_decode_slice_keys cuts contexts into
     whole chunks, kMergeBatch (8) slices of 2 to 8 chunks for few groups at head sizes 64 and
     128, one slice for a handful of
-    short contexts, at least two otherwise, never below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles;
+    short contexts, at least two otherwise, never below 8 chunks; rh_gemv_f16_split_plan splits K in two only for long K on few row tiles above 16 tokens;
     rh_gemv_int8_row_stride pads rows that are a multiple of 2 KB."""
     L = _lib.lib()
     for D in (16, 32, 64, 128):
@@ -167,6 +167,6 @@ def test_work_planners_follow_their_rules():
     assert L.rh_decode_chunk_keys(96) == -1
     assert [L.rh_gemv_f16_split_plan(T, K, N) for T, K, N in
             [(32, 5632, 2048), (1, 5632, 2048), (32, 2048, 2048), (32, 4096, 4096), (8, 14336, 4096), (1, 4096, 1024)]] \
-        == [2, 2, 1, 1, 1, 2]
+        == [2, 1, 1, 1, 1, 1]
     assert L.rh_gemv_f16_split_plan(0, 64, 64) == -1
     assert [L.rh_gemv_int8_row_stride(K) for K in (4096, 14336, 2048, 576, 100)] == [4352, 14592, 2304, 576, 112]
