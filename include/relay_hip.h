@@ -233,10 +233,9 @@ int rh_gemv_f16_split_plan(int T, int K, int N);
  *             sum of squares in double (rh_rmsnorm's arithmetic);
  *   _silu:    gu fp32 [T, 2K] (gate | up) -> fp16(g / (1 + exp(-g)) * u) (rh_silu_mul's).
  * Requires rh_gemv_f16_fused_fits(T, K) (T * (K + 8) fp16 values fit 64 KB of LDS).
- * At 1-16 tokens these (and rh_gemv_f16_qkv / _rmsnorm_qkv) run a whole-line kernel whose
- * row groups and wave split can differ from rh_gemv_f16's, so they agree with the two-launch
- * chain within the fp32 accumulation bound; at 17-32 tokens, where both take the 16-row
- * tile, bit for bit. */
+ * These (and rh_gemv_f16_qkv / _rmsnorm_qkv) run a whole-line kernel whose row groups and
+ * wave split can differ from rh_gemv_f16's, so they agree with the two-launch chain within
+ * the fp32 accumulation bound. */
 int rh_gemv_f16_rmsnorm(const void* w16, int64_t ldw, const float* x, const float* norm_w, float eps, float* y,
                         int T, int K, int N, float beta, void* stream);
 int rh_gemv_f16_silu(const void* w16, int64_t ldw, const float* gu, float* y, int T, int K, int N, float beta,

@@ -1065,7 +1065,7 @@ int launch_whole_line(const void* w, int64_t ldw, const void* scale, const void*
                       float* y, int T, int K, int N, float beta, hipStream_t s, const RopeArgs& ra) {
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv: T * (K + 8) fp16 activations exceed the fused path's LDS");
-  RH_REQUIRE(T >= 1 && T <= 16, "gemv: the whole-line kernel takes 1-16 tokens");
+  RH_REQUIRE(T >= 1 && T <= 32, "gemv: the whole-line kernel takes 1-32 tokens");
   const bool rt1 = EPI == kStore && (N + 7) / 8 <= 256;
   const int groups = rt1 ? (N + 7) / 8 : (N + 15) / 16;
   const bool w16 = rt1 || groups < 256;
@@ -1073,21 +1073,27 @@ int launch_whole_line(const void* w, int64_t ldw, const void* scale, const void*
   RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_m8_fused_kernel<WAVES, DEPTH, W16, F16_SCALE, PRO, EPI, RTV, NBV>),      \
                                    dim3(groups), dim3(WAVES * kWave), staged, s, w, ldw, scale, x, norm_w, eps, y, T, K, \
                                    N, beta, ra))
-#define RH_WL_NB(RTV, NBV)                   \
-  if (w16) {                                 \
-    if (W16) RH_WL(16, 4, RTV, NBV);         \
-    else RH_WL(16, 1, RTV, NBV);             \
-  } else {                                   \
-    if (W16) RH_WL(8, 4, RTV, NBV);          \
-    else RH_WL(8, 2, RTV, NBV);              \
+#define RH_WL_NB(RTV, NBV)                                   \
+  if (w16) {                                                 \
+    if constexpr (W16) RH_WL(16, (NBV <= 2 ? 4 : 2), RTV, NBV); \
+    else RH_WL(16, 1, RTV, NBV);                             \
+  } else {                                                   \
+    if constexpr (W16) RH_WL(8, (NBV <= 2 ? 4 : 2), RTV, NBV);  \
+    else RH_WL(8, (NBV <= 2 ? 2 : 1), RTV, NBV);             \
   }
+#define RH_WL_T(RTV)                    \
+  if (T <= 8) { RH_WL_NB(RTV, 1) }      \
+  else if (T <= 16) { RH_WL_NB(RTV, 2) } \
+  else if (T <= 24) { RH_WL_NB(RTV, 3) } \
+  else { RH_WL_NB(RTV, 4) }
   if constexpr (EPI == kStore) {
     if (rt1) {
-      if (T <= 8) { RH_WL_NB(1, 1) } else { RH_WL_NB(1, 2) }
+      RH_WL_T(1)
       return 0;
     }
   }
-  if (T <= 8) { RH_WL_NB(2, 1) } else { RH_WL_NB(2, 2) }
+  RH_WL_T(2)
+#undef RH_WL_T
 #undef RH_WL_NB
 #undef RH_WL
   return 0;
@@ -1103,24 +1109,11 @@ int launch_fused(const int8_t* w8, int64_t ldw, const void* scale, const void* x
   const size_t staged = PRO == kPlain ? 0 : static_cast<size_t>(T) * (K + 8) * sizeof(half_t);
   RH_REQUIRE(staged <= kFusedLdsBytes, "gemv_int8: T * (K + 8) fp16 activations exceed the fused path's LDS");
   const int tiles = (N + 15) / 16;
-  // 1-16 tokens without the SiLU producer: the whole-line form (a one-token vector-ALU form
-  // behind the producers made TinyLlama int8 decode steps slower).
+  // 1-16 tokens without the SiLU producer, and the qkv epilogue up to 32: the whole-line form
+  // (a one-token vector-ALU form behind the producers made TinyLlama int8 decode steps slower).
   if constexpr (PRO != kSiluMul) {
-    if (T <= 16)
+    if (T <= 16 || (EPI == kRope && T <= 32))
       return launch_whole_line<false, F16_SCALE, PRO, EPI>(w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, s, ra);
-  }
-  if constexpr (PRO == kPlain) {
-    if (T > kMaxTokens) {  // the qkv epilogue alone, 17-32 tokens: two column blocks
-      if (tiles < 256) {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 2, 1, F16_SCALE, PRO, EPI>), dim3(tiles),
-                                         dim3(16 * kWave), 0, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16,
-                                         ra));
-      } else {
-        RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<8, 2, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(8 * kWave),
-                                         0, s, w8, ldw, scale, xin, norm_w, eps, y, T, K, N, beta, 16, ra));
-      }
-      return 0;
-    }
   }
   if (tiles < 256) {
     RH_TRY_LAUNCH(hipLaunchKernelGGL((gemv_int8_kernel<16, 1, 1, F16_SCALE, PRO, EPI>), dim3(tiles), dim3(16 * kWave),
@@ -1467,11 +1460,11 @@ static int gemv_f16_launch(const void* w16, int64_t ldw, const void* x, const fl
     return launch_f16_t1(wt, ldw, static_cast<const half_t*>(x), y, K, N, beta, s);
   if (PRO == kPlain && EPI == kStore && ksplit == 1 && f16_m8_takes(T))
     return launch_f16_m8(wt, ldw, static_cast<const half_t*>(x), y, T, K, N, beta, s);
-  if (PRO == kPlain && EPI == kStore && ksplit == 1 && T >= 9 && T <= 16)
+  if (PRO == kPlain && EPI == kStore && ksplit == 1 && T >= 9)
     return launch_whole_line<true, false, kPlain, kStore>(wt, ldw, nullptr, x, nullptr, 0.0f, y, T, K, N, beta, s, ra);
   if constexpr (PRO != kPlain || EPI != kStore) {
     // A producer or the qkv epilogue at 1-16 tokens: the whole-line fused kernel.
-    if (ksplit == 1 && T <= 16)
+    if (ksplit == 1 && T <= 32)
       return launch_whole_line<true, false, PRO, EPI>(wt, ldw, nullptr, x, norm_w, eps, y, T, K, N, beta, s, ra);
   }
   if (T <= kMaxTokens) {

@@ -408,7 +408,12 @@ void HipBackend::gemm_f16(const std::uint16_t* W, const std::uint16_t* x, float*
                                 rocblas_gemm_algo_standard, 0, 0));
 }
 
-bool HipBackend::skinny(int K, int N, int T) { return K % 16 == 0 && T <= 16; }
+bool HipBackend::skinny(int K, int N, int T) {
+  // Up to 16 tokens always; 17-32 tokens on matrices under 4 Mi weights (the whole-line
+  // kernel: SmolLM2-135M 32 x 640 decode step 1.50 -> 1.27 ms; TinyLlama's 2048 x 2048 o
+  // projection at 32 tokens 1.569 -> 1.592 ms against the library's).
+  return K % 16 == 0 && (T <= 16 || (T <= 32 && static_cast<std::int64_t>(N) * K < (std::int64_t{1} << 22)));
+}
 
 bool HipBackend::fused(const DeviceMatrix& W, int T, bool int8_ok) const {
   // Normalisation / activation folded into the skinny fp16 product, up to 16 tokens, when its
@@ -624,16 +629,17 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
                                          D, layout_.block_size, stream_));
     } else if (L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 && T <= 32 && (QKV + 15) / 16 <= 256) {
       // int8: the projection and qkv_post in one launch (its 16-row tiles in one round;
-      // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms; at 17-32 tokens two 16-token
-      // column blocks).
+      // TinyLlama int8 b = 16 decode step 1.369 -> 1.352 ms on the 16-row tile, whose place
+      // the whole-line kernel has taken).
       if (!attn_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_int8_qkv(L.wqkv.i8.p, L.wqkv.ldw, L.wqkv.scale.p, 0, xn_.p, qkv_.p, T, H, bias, inv_freq_.p,
                                 d_pos, d_seq, d_toff, d_tab, kc, vc, q_out, q_scale, c_.heads, c_.kv_heads, D,
                                 layout_.block_size, stream_));
     } else if (!L.wqkv.i8.p && D % 16 == 0 && H % 16 == 0 &&
                (T <= 16 || (T <= rh_gemv_f16_max_tokens() && QKV <= 4096)) && rh_gemv_f16_split_plan(T, H, QKV) == 1) {
-      // (17-32 tokens: TinyLlama's 2560-row qkv 11.1 us here against 9.5 + 3.0 us for the
-      // library product and a separate qkv_post.)
+      // (17-32 tokens: TinyLlama's 2560-row qkv 11.1 us on the 16-row tile against 9.5 + 3.0 us
+      // for the library product and a separate qkv_post; the whole-line kernel since: 32 x 2048
+      // decode step 1.638 -> 1.573-1.603 ms.)
       // The projection and qkv_post in one launch (the RMSNorm cannot be folded in here).
       if (!attn_xn_ready) RH_CHECK(rh_rmsnorm(x_.p, nullptr, T, L.attn_norm.p, H, eps, xn_.p, stream_));
       RH_CHECK(rh_gemv_f16_qkv(L.wqkv.f16.p, H, xn_.p, qkv_.p, T, H, bias, inv_freq_.p, d_pos, d_seq, d_toff, d_tab,

@@ -19,15 +19,15 @@ EPS32 = 2.0 ** -24
 
 def whole_line(T, N, K):
     """Whether rh_gemv_f16 takes a whole-line kernel (the vector-ALU one at one token from 2 Mi
-    weights, the 8-row MFMA one at 1-8 tokens otherwise, the fused kernel's at 9-16) instead
-    of the 16-row MFMA tile."""
-    return 1 <= T <= 16
+    weights, the 8-row MFMA one at 1-8 tokens otherwise, the fused kernel's at 9-32) instead
+    of the 16-row MFMA tile (which only the K split runs now)."""
+    return 1 <= T <= 32
 
 
 def fused_differs(T, N, K):
     """Whether a fused launch (producer or qkv epilogue) and the plain launch of the chain it
-    replaces may sum in different orders: at 1-16 tokens both run whole-line kernels, whose
-    row groups and wave splits can differ; above that both take the 16-row tile."""
+    replaces may sum in different orders: both run whole-line kernels, whose row groups and
+    wave splits can differ."""
     return whole_line(T, N, K)
 
 

@@ -22,10 +22,10 @@ EPS32 = 2.0 ** -24
 
 def vector_alu(T, N, K):
     """Whether a fused int8 launch and the plain launch of the chain it replaces may sum in
-    different orders: both run whole-line MFMA kernels at 1-16 tokens (8 or 16 rows per
-    workgroup, their own wave splits; rh_gemv_int8 keeps its row-tile kernels on more than
-    6144 rows at 9-16)."""
-    return 1 <= T <= 16
+    different orders: the fused forms run the whole-line MFMA kernel at 1-16 tokens (the qkv
+    form up to 32) with their own row groups and wave splits, while rh_gemv_int8 keeps its
+    row-tile kernels above 16 tokens and on more than 6144 rows at 9-16."""
+    return 1 <= T <= 32
 
 
 def run(torch, dev, w8, scale, x_bits, beta=0.0, y0=None, f16_scale=False, ldw=None):
