@@ -72,3 +72,20 @@ def test_relay_engine_on_hip_with_fixture_models(dev, fixture):
     assert out["tokens_equal"]
     assert out["worst_rel"] < 2e-2
     assert out["steps"][0] == out["steps"][1]
+
+
+@pytest.mark.parametrize("blocks,block_size,mbt", [(18, 4, 64), (128, 1, 512), (8, 32, 512)])
+def test_relay_batching_schedules_keep_greedy_tokens(dev, blocks, block_size, mbt):
+    """The schedules of relay's test_batching.cpp:97-120 (a cache of 18 blocks of 4 tokens
+    that forces preemption and recompute; block sizes 1 and 32) with its prompt lengths and
+    token counts, all greedy: the HIP backend's tokens equal relay's CPU backend's under each
+    schedule (the sampled requests of that program are not held bitwise across schedules on
+    a non-exact backend, test_relay_suites_hip.py)."""
+    reqs = ",".join(f"{n}:{3 + (i * 5) % 11}" for i, n in enumerate([1, 5, 17, 33, 2, 48, 9, 16]))
+    out = engine(os.path.join(FIX, "llama-gqa-tied-bf16"), blocks, block_size, mbt, 8, False, reqs, 11)
+    assert out["tokens_equal"]
+    assert out["worst_rel"] < 2e-2
+    assert out["steps"][0] == out["steps"][1] and out["preemptions"][0] == out["preemptions"][1]
+    if blocks == 18:
+        assert out["preemptions"][0] > 0
+
