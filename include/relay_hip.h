@@ -187,12 +187,22 @@ int rh_gemv_int8_rmsnorm_qkv(const int8_t* w8, int64_t ldw, const void* scale, i
                              int kv_heads, int head_dim, int block_size, void* stream);
 
 /* act[t, a] = fp16(silu(g) * u), g and u the rows a and I + a of rh_gemv_int8's product of
- * the fused gate/up matrix W8 [2 I, K] (scale [2 I]) with x fp16 [T, K], for 1 <= T <= 8;
- * act fp16 [T, I]. The same bits as rh_gemv_int8 into an fp32 [T, 2 I] buffer followed by
- * rh_silu_mul, in one launch (each workgroup holds both halves of its outputs). No
- * counterpart in relay (gemm then silu_mul_kernel, cuda_backend.cu:590-591). */
+ * the fused gate/up matrix W8 [2 I, K] (scale [2 I]) with x fp16 [T, K], for 1 <= T <= 16;
+ * act fp16 [T, I]. At 1-8 tokens the same bits as rh_gemv_int8 into an fp32 [T, 2 I] buffer
+ * followed by rh_silu_mul, in one launch (each workgroup holds both halves of its
+ * outputs); at 9-16 tokens the whole-line kernel, whose sums agree with rh_gemv_int8's within
+ * the fp32 accumulation bound. No counterpart in relay (gemm then silu_mul_kernel,
+ * cuda_backend.cu:590-591). */
 int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16, const void* x,
                               void* act, int T, int K, int I, void* stream);
+
+/* The fp16 counterpart, 1 <= T <= 32: act[t, a] = fp16(silu(g) * u) of the fused gate/up
+ * matrix W16 [2 I, K] (rows ldw elements apart) with x fp16 [T, K], on the whole-line kernel
+ * with SiLU·mul in its epilogue; agrees with rh_gemv_f16 + rh_silu_mul within the fp32
+ * accumulation bound. No counterpart in relay (cublasGemmEx then silu_mul_kernel,
+ * cuda_backend.cu:588-589). */
+int rh_gemv_f16_gate_up_silu(const void* w16, int64_t ldw, const void* x, void* act, int T, int K, int I,
+                             void* stream);
 
 /* rh_gemv_int8_gate_up_silu with relay's RMSNorm of x folded in: act[t, a] = fp16(silu(g) *
  * u) of the product with xn = fp16(norm_w * (x * 1/sqrt(mean(x^2) + eps))), x fp32 [T, K] (the

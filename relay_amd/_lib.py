@@ -61,6 +61,7 @@ SIGNATURES = {
     "rh_gemv_int8_rmsnorm": (I, [P, I64, P, I, P, P, F, P, I, I, I, F, P]),
     "rh_gemv_int8_silu": (I, [P, I64, P, I, P, P, I, I, I, F, P]),
     "rh_gemv_int8_gate_up_silu": (I, [P, I64, P, I, P, P, I, I, I, P]),
+    "rh_gemv_f16_gate_up_silu": (I, [P, I64, P, P, I, I, I, P]),
     "rh_gemv_int8_rmsnorm_gate_up_silu": (I, [P, I64, P, I, P, P, F, P, I, I, I, P]),
     "rh_gemv_int8_qkv": (I, [P, I64, P, I, P, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),
     "rh_gemv_int8_rmsnorm_qkv": (I, [P, I64, P, I, P, P, F, P, I, I, P, P, P, P, P, P, P, P, P, F, I, I, I, I, P]),

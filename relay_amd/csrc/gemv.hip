@@ -885,7 +885,6 @@ template <int WAVES, int DEPTH, bool W16, bool F16_SCALE, int PRO, int EPI, int 
 __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     const void* __restrict__ wq, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
     const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
-  static_assert(!W16 || EPI != kSilu, "the SiLU epilogue is the int8 form's");
   static_assert(RT == 2 || (RT == 1 && EPI == kStore), "the qkv and SiLU epilogues pair rows in 16-row tiles");
   constexpr int KS = W16 ? 64 : 128;  // k per step
   const int8_t* w8 = static_cast<const int8_t*>(wq);
@@ -1252,7 +1251,7 @@ extern "C" int rh_gemv_int8(const int8_t* w8, int64_t ldw, const void* scale, in
 
 extern "C" int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16,
                                          const void* x, void* act, int T, int K, int I, void* stream) {
-  RH_REQUIRE(T >= 1 && T <= 8, "gemv_int8_gate_up_silu: T must be in 1..8");
+  RH_REQUIRE(T >= 1 && T <= 16, "gemv_int8_gate_up_silu: T must be in 1..16");
   RH_REQUIRE(K > 0 && I > 0 && K % 16 == 0, "gemv_int8_gate_up_silu: K must be a positive multiple of 16");
   RH_REQUIRE(ldw >= K && ldw % 16 == 0 && ldw < (1 << 21),
              "gemv_int8_gate_up_silu: ldw must be >= K, < 2^21 and a multiple of 16");
@@ -1262,8 +1261,27 @@ extern "C" int rh_gemv_int8_gate_up_silu(const int8_t* w8, int64_t ldw, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
   half_t* a = static_cast<half_t*>(act);
+  if (T > 8) {  // two 8-token column blocks of the whole-line kernel, SiLU in its epilogue
+    float* out = reinterpret_cast<float*>(act);
+    return scale_is_f16 ? launch_whole_line<false, true, kPlain, kSilu>(w8, ldw, scale, x, nullptr, 0.0f, out, T, K,
+                                                                        2 * I, 0.0f, s, RopeArgs{})
+                        : launch_whole_line<false, false, kPlain, kSilu>(w8, ldw, scale, x, nullptr, 0.0f, out, T, K,
+                                                                         2 * I, 0.0f, s, RopeArgs{});
+  }
   return scale_is_f16 ? launch_m8_silu<true>(w8, ldw, scale, xh, a, T, K, I, s)
                       : launch_m8_silu<false>(w8, ldw, scale, xh, a, T, K, I, s);
+}
+
+extern "C" int rh_gemv_f16_gate_up_silu(const void* w16, int64_t ldw, const void* x, void* act, int T, int K, int I,
+                                        void* stream) {
+  RH_REQUIRE(T >= 1 && T <= 32, "gemv_f16_gate_up_silu: T must be in 1..32");
+  RH_REQUIRE(K > 0 && I > 0 && K % 16 == 0, "gemv_f16_gate_up_silu: K must be a positive multiple of 16");
+  RH_REQUIRE(ldw >= K && ldw % 8 == 0, "gemv_f16_gate_up_silu: ldw must be >= K and a multiple of 8");
+  RH_REQUIRE(w16 != nullptr && x != nullptr && act != nullptr, "gemv_f16_gate_up_silu: missing pointer");
+  RH_REQUIRE((reinterpret_cast<uintptr_t>(w16) | reinterpret_cast<uintptr_t>(x)) % 16 == 0,
+             "gemv_f16_gate_up_silu: W16 and x must be 16-byte aligned");
+  return launch_whole_line<true, false, kPlain, kSilu>(w16, ldw, nullptr, x, nullptr, 0.0f, static_cast<float*>(act), T,
+                                                       K, 2 * I, 0.0f, static_cast<hipStream_t>(stream), RopeArgs{});
 }
 
 extern "C" int rh_gemv_int8_rmsnorm_gate_up_silu(const int8_t* w8, int64_t ldw, const void* scale, int scale_is_f16,

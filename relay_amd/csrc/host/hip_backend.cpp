@@ -687,7 +687,11 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
       RH_CHECK(rh_gemv_f16_rmsnorm(L.w_gate_up.f16.p, H, x_.p, L.mlp_norm.p, eps, gu_.p, T, H, 2 * I, 0.0f,
                                    stream_));
     } else {
+      // (int8 at 9-16 tokens: level at b = 12, 1.29 -> 1.305 ms at b = 16 on TinyLlama.)
       const bool i8_silu = L.w_gate_up.i8.p && T <= 8 && H % 16 == 0;
+      // fp16 where gemm() would take the whole-line product: the same kernel with SiLU·mul
+      // in its epilogue.
+      const bool f16_silu = !L.w_gate_up.i8.p && skinny(H, 2 * I, T) && T <= 32;
       if (i8_silu && !mlp_xn_ready && rh_gemv_f16_fused_fits(T, H) && (I + 7) / 8 < 256) {
         // The RMSNorm, the int8 product and SiLU·mul in one launch, where its workgroups
         // (8 outputs each) fit one round on the CUs: every workgroup normalises x again, which
@@ -713,9 +717,12 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
           act_ready = true;
         } else if (i8_silu) {
           // gemm()'s product at this T (the int8 GEMV) with SiLU·mul in its epilogue: one
-          // launch fewer per layer, the same bits.
+          // launch fewer per layer (the same bits at 1-8 tokens).
           RH_CHECK(rh_gemv_int8_gate_up_silu(L.w_gate_up.i8.p, L.w_gate_up.ldw, L.w_gate_up.scale.p, 0, xn_.p,
                                              act_.p, T, H, I, stream_));
+          act_ready = true;
+        } else if (f16_silu) {
+          RH_CHECK(rh_gemv_f16_gate_up_silu(L.w_gate_up.f16.p, H, xn_.p, act_.p, T, H, I, stream_));
           act_ready = true;
         } else {
           gemm(L.w_gate_up, xn_.p, gu_.p, T, 0.0f);
@@ -726,7 +733,7 @@ std::size_t HipBackend::enqueue_forward(const ForwardBatch& batch, LayerObserver
     // small (TinyLlama fp16 decode, I = 5632: b = 2 1.085 -> 1.063 ms, b = 4 1.177 -> 1.103
     // with the separate SiLU launch, level at b = 1 and 8; SmolLM2-135M, I = 1536, b = 1
     // fused: 1087 against 1048 tok/s).
-    if (fused(L.w_down, T) && T * I <= 8192) {
+    if (!act_ready && fused(L.w_down, T) && T * I <= 8192) {
       RH_CHECK(rh_gemv_f16_silu(L.w_down.f16.p, I, gu_.p, x_.p, T, I, H, 1.0f, stream_));  // x += act W_down^T
     } else {
       if (!act_ready) RH_CHECK(rh_silu_mul(gu_.p, T, I, act_.p, stream_));

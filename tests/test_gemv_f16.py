@@ -332,3 +332,49 @@ def f16_close(a_bits, b_bits, tol, name):
     vb = b_bits.view(np.float16).astype(np.float64)
     lim = tol + 2.0 ** -10 * np.maximum(np.abs(va), np.abs(vb)) + 2.0 ** -24
     assert (np.abs(va - vb) <= lim).all(), name
+
+
+@pytest.mark.parametrize("T,I,K", [(1, 5632, 2048), (4, 1536, 576), (8, 5632, 2048), (12, 1536, 576), (16, 5632, 2048),
+                                   (24, 1536, 576), (32, 1536, 576), (3, 102, 160), (17, 250, 1024)])
+def test_gate_up_silu_matches_the_chain(torch_mod, dev, T, I, K):
+    """rh_gemv_f16_gate_up_silu (the whole-line kernel with SiLU·mul in its epilogue, gate and
+    up rows of each output in one workgroup) against rh_gemv_f16 over the fused [gate; up]
+    matrix + rh_silu_mul: within the fp32 accumulation bound of g and u carried through
+    SiLU·mul plus one fp16 rounding; I not a multiple of 8 included."""
+    from relay_amd import _lib
+
+    torch = torch_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(T * 17 + I + K)
+    w16 = (rng.standard_normal((2 * I, K)) * 0.05).astype(np.float16)
+    x = (rng.standard_normal((T, K)) * 2).astype(np.float16)
+    W = torch.from_numpy(w16.view(np.int16)).to(dev)
+    X = torch.from_numpy(x.view(np.int16)).to(dev)
+    gu = torch.empty((T, 2 * I), device=dev)
+    act_a = torch.empty((T, I), dtype=torch.int16, device=dev)
+    act_b = torch.full((T, I), 0x7E00, dtype=torch.int16, device=dev)
+    print(f"gemv_f16_gate_up_silu: T={T} I={I} K={K}", flush=True)
+    _lib.check(L.rh_gemv_f16(W.data_ptr(), K, X.data_ptr(), gu.data_ptr(), T, K, 2 * I, 0.0, None), "rh_gemv_f16")
+    _lib.check(L.rh_silu_mul(gu.data_ptr(), T, I, act_a.data_ptr(), None), "rh_silu_mul")
+    _lib.check(L.rh_gemv_f16_gate_up_silu(W.data_ptr(), K, X.data_ptr(), act_b.data_ptr(), T, K, I, None),
+               "rh_gemv_f16_gate_up_silu")
+    torch.cuda.synchronize()
+    exact = x.astype(np.float64) @ w16.astype(np.float64).T
+    err = gemv_bound(w16, x) + 2 * EPS32 * np.abs(exact)
+    g, u, dg, du = exact[:, :I], exact[:, I:], err[:, :I], err[:, I:]
+    silu = g / (1.0 + np.exp(-g))
+    f16_close(act_a.cpu().numpy(), act_b.cpu().numpy(), 2 * (1.1 * np.abs(u) * dg + np.abs(silu) * du + dg * du), "act")
+    want = (silu * u).astype(np.float64)
+    got = act_b.cpu().numpy().view(np.float16).astype(np.float64)
+    assert (np.abs(got - want) <= 1.1 * np.abs(u) * dg + np.abs(silu) * du + dg * du
+            + 2.0 ** -10 * np.abs(want) + 2.0 ** -24).all()
+
+
+def test_gate_up_silu_limits(dev):
+    from relay_amd import _lib
+
+    L = _lib.lib()
+    assert L.rh_gemv_f16_gate_up_silu(None, 64, None, None, 33, 64, 32, None) != 0
+    assert "T must be in 1..32" in _lib.last_error()
+    assert L.rh_gemv_f16_gate_up_silu(None, 64, None, None, 4, 64, 32, None) != 0
+    assert "missing pointer" in _lib.last_error()
