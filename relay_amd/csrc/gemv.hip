@@ -886,6 +886,7 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     const void* __restrict__ wq, int64_t ldw, const void* __restrict__ scale, const void* __restrict__ xin,
     const float* __restrict__ norm_w, float eps, float* y, int T, int K, int N, float beta, RopeArgs ra) {
   static_assert(RT == 2 || (RT == 1 && EPI == kStore), "the qkv and SiLU epilogues pair rows in 16-row tiles");
+  static_assert(WAVES >= 4, "the qkv and SiLU epilogues take one thread per (token, pair) for up to 32 tokens");
   constexpr int KS = W16 ? 64 : 128;  // k per step
   const int8_t* w8 = static_cast<const int8_t*>(wq);
   const int64_t ldb = W16 ? 2 * ldw : ldw;  // row stride in bytes
@@ -999,11 +1000,14 @@ __global__ __launch_bounds__(WAVES * kWave) void gemv_int8_m8_fused_kernel(
     return W16 ? v : v * row_scale(min(out_row(m >> 3, m & 7), N - 1));
   };
   if constexpr (EPI == kStore) {
-    const int t = threadIdx.x / (8 * RT), m = threadIdx.x % (8 * RT);
-    const int n = 8 * RT * blockIdx.x + m;
-    if (threadIdx.x < 8 * RT * T && n < N) {
-      float* dst = y + static_cast<int64_t>(t) * N + n;
-      *dst = value(t, m) + (beta != 0.0f ? beta * *dst : 0.0f);
+    // One (token, row) output per thread; 8 RT T can exceed the workgroup at 17-32 tokens.
+    for (int i = threadIdx.x; i < 8 * RT * T; i += WAVES * kWave) {
+      const int t = i / (8 * RT), m = i % (8 * RT);
+      const int n = 8 * RT * blockIdx.x + m;
+      if (n < N) {
+        float* dst = y + static_cast<int64_t>(t) * N + n;
+        *dst = value(t, m) + (beta != 0.0f ? beta * *dst : 0.0f);
+      }
     }
   } else if constexpr (EPI == kSilu) {
     // Thread (t, j) writes act[t, a0 + j]: gate slot 8 (j / 4) + j % 4, up slot 4 further
