@@ -316,7 +316,8 @@ int rh_gemm_w8_gate_up_silu(const int8_t* w8, int64_t ldw, const float* scale, c
 
 /* rh_gemm_w8 for 1 <= T <= 64 with a 128-row x 32-token tile (64 tokens above 32) and K cut
  * into ksplit ranges (1 <= ksplit <= 8, at most K / 64), so that decode batches of 17-64
- * tokens read the int8 weights once on enough workgroups; workspace as for
+ * tokens read the int8 weights once on enough workgroups: 128-k steps where K is a multiple
+ * of 128 and ksplit <= K / 128, 64-k steps otherwise; workspace as for
  * rh_gemm_w8_split. No counterpart in relay (dequantize + cublasGemmEx,
  * cuda_backend.cu:718-722). */
 int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const void* x, float* y, int T, int K, int N,

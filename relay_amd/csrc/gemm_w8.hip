@@ -618,14 +618,24 @@ extern "C" int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x,
   const half_t* xh = static_cast<const half_t*>(x);
   // No scale is read: the partials are the raw sums. The tile is the one the merging entry
   // point takes for this T.
+  if (T <= 64 && w8_wide_fits(K, ksplit))
+    return T <= 32 ? launch_w8_wide<1>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace)
+                   : launch_w8_wide<2>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
   if (T <= 32) return launch_w8_tile<1, 1, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
   if (T <= 64) return launch_w8_tile<1, 2, 4>(w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
   return launch_w8_cfg(w8_cfg_for(T, K, N, ksplit), w8, ldw, nullptr, xh, nullptr, T, K, N, 0.0f, st, -ksplit, workspace);
 }
 
-// 17-64 tokens: 128 rows x 32 tokens (x 64 above 32 tokens), four waves per SIMD, K cut
-// until the row tiles x ranges reach 256 workgroups (at most 8 ranges of >= 4 steps).
-// Measured (us, in isolation, T = 32; the GEMV and the previous 128-row x 64-token tile in
+// 17-64 tokens: the wide-step kernel with a 32-token tile (64 above 32 tokens) where K is
+// a multiple of 128, else the 64-k tile kernel (128 rows x 32 or 64 tokens, four waves per
+// SIMD, K cut until the row tiles x ranges reach 256 workgroups, at most 8 ranges of >= 4
+// steps). The wide-step kernel, measured against the tile kernel at the tile kernel's plan
+// (us, in isolation, merge launch included; T = 32 / 64): 28672 x 4096 31.2 / 38.1 against
+// 35.8 / 45.6, 4096 x 14336 20.4 / 24.7 against 22.7 / 28.9, 6144 x 4096 14.7 / 17.9 against
+// 17.5 / 22.0, 11264 x 2048 14.8 against 17.7, 2048 x 5632 13.2 / 15.6 against 13.5 / 16.2;
+// TinyLlama int8 decode steps 1.676 -> 1.617 ms at b = 32, 1.587 -> 1.540 at 24, 1.464 ->
+// 1.424 at 17. (Loading W four steps ahead in the tile kernel instead: 1-7% slower.)
+// The tile kernel (us, in isolation, T = 32; the GEMV and a 128-row x 64-token tile in
 // brackets): 28672 x 4096 32.8 [-, 34.0], 4096 x 14336 24.3 [-, 26.9], TinyLlama 2048 x
 // 5632 12.3 [15.2, 14.9], 11264 x 2048 15.0 [15.7, 17.7]; on K <= 4096 matrices of <= 6144
 // rows the GEMV stays ahead (4096 x 4096: 12.5 against 13.5).
@@ -636,6 +646,14 @@ extern "C" int rh_gemm_w8_split_plan(int T, int K, int N) {
   // (One range from 64 row tiles up, to save the merge launch, made the TinyLlama int8
   // 32 x 2048 decode step slower: 1.80 -> 1.91 ms.)
   const int tiles = (N + 127) / 128;
+  if (K % 128 == 0) {
+    // The wide-step kernel: as many ranges (of >= 2 steps) as keep the grid within one
+    // workgroup per CU; one more round of a few workgroups costs more than the ranges save
+    // (T = 32, 11264 x 2048: 2 ranges 14.8 us, 3 ranges 18.4).
+    int ks = std::max(1, std::min(8, 256 / tiles));
+    while (ks > 1 && (K / 128) / ks < 2) --ks;
+    return N % 4 ? 1 : ks;
+  }
   int ks = std::min(8, (256 + tiles - 1) / tiles);
   while (ks > 1 && (K / 64) / ks < 4) --ks;
   return N % 4 ? 1 : ks;
@@ -652,6 +670,9 @@ extern "C" int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* sca
   RH_REQUIRE(ksplit == 1 || N % 4 == 0, "gemm_w8_skinny: ksplit > 1 needs N a multiple of 4");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const half_t* xh = static_cast<const half_t*>(x);
+  if (w8_wide_fits(K, ksplit))
+    return T <= 32 ? launch_w8_wide<1>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace)
+                   : launch_w8_wide<2>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
   if (T <= 32) return launch_w8_tile<1, 1, 4>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
   return launch_w8_tile<1, 2, 4>(w8, ldw, scale, xh, y, T, K, N, beta, st, ksplit, workspace);
 }

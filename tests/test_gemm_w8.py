@@ -228,7 +228,7 @@ def run_skinny(torch, dev, q, scale, x, ks, beta=0.0, y0=None, ldw=None):
 
 
 @pytest.mark.parametrize("ks", [1, 2, 3, 8])
-@pytest.mark.parametrize("T,N,K", [(1, 64, 1024), (17, 200, 2048), (48, 1000, 4096), (64, 4096, 14336 // 4),
+@pytest.mark.parametrize("T,N,K", [(1, 64, 1024), (17, 200, 2048), (48, 1000, 4096), (64, 4096, 14336 // 4), (20, 256, 640),
                                    (33, 132, 1088)])
 def test_skinny_split_k_matches_float64(torch_mod, dev, T, N, K, ks):
     """rh_gemm_w8_skinny at any K split (ranges of whole 64-k steps) stays within the
@@ -246,7 +246,7 @@ def test_skinny_accumulates_and_limits(torch_mod, dev):
     y0 = np.random.default_rng(4).standard_normal((40, 300)).astype(np.float32)
     check(run_skinny(torch_mod, dev, q, scale, x, 4, beta=1.0, y0=y0), q, scale, x, beta=1.0, y0=y0)
     L = _lib.lib()
-    assert L.rh_gemm_w8_split_plan(48, 14336, 4096) == 8 and L.rh_gemm_w8_split_plan(48, 4096, 28672) == 2
+    assert L.rh_gemm_w8_split_plan(48, 14336, 4096) == 8 and L.rh_gemm_w8_split_plan(48, 4096, 28672) == 1
     assert L.rh_gemm_w8_split_plan(65, 4096, 4096) == -1
     assert L.rh_gemm_w8_skinny(None, 128, None, None, None, 65, 128, 64, 0.0, 1, None, None) != 0
     assert "T must be in 1..64" in _lib.last_error()
