@@ -330,6 +330,11 @@ int rh_gemm_w8_skinny(const int8_t* w8, int64_t ldw, const float* scale, const v
  * the scale, with the arithmetic of the two-launch chain (same bits). */
 int rh_gemm_w8_partials(const int8_t* w8, int64_t ldw, const void* x, int T, int K, int N, int ksplit,
                         float* workspace, void* stream);
+/* The split for rh_gemm_w8_partials when the consumer merges (-1 for bad arguments): the
+ * rh_gemm_w8_plan split, except above 64 tokens where that plan runs the product unsplit on
+ * fewer than 256 workgroups; there the K ranges the timing model prices lowest with the
+ * merge done by the consumer (its extra partial reads only). No counterpart in relay. */
+int rh_gemm_w8_partials_plan(int T, int K, int N);
 
 /* act[t, i] = silu(g) * up of the merged gate_up partials (rows [0, I) gate, [I, 2I) up;
  * act fp16 [T, I], I a multiple of 8): rh_gemm_w8_skinny's merge followed by rh_silu_mul in

@@ -78,6 +78,7 @@ SIGNATURES = {
     "rh_w8_merge_rmsnorm": (I, [P, I, I, I, P, P, P, F, P, P]),
     "rh_w8_merge_rmsnorm_fits": (I, [I]),
     "rh_gemm_w8_plan": (I, [I, I, I]),
+    "rh_gemm_w8_partials_plan": (I, [I, I, I]),
     "rh_gemm_w8_kernel": (I, [I, I, I, I]),
     "rh_gemm_w8_gate_up_silu": (I, [P, I64, P, P, P, I, I, I, P]),
     "rh_gemm_w8_split_plan": (I, [I, I, I]),

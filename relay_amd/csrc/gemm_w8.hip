@@ -461,7 +461,10 @@ W8Plan w8_tile_plan(int T, int K, int N) {
 // 2.16 us + 1.53 us per million partial sums read and written. Choosing the minimum of the
 // model picks a kernel within 1.3% of the measured best on average over those points
 // (worst 11%), against 22% above it for the previous plan.
-double w8_model_us(int cfg, int T, int K, int N, int ks) {
+// With consumer_merge the partials are added by the product's consumer (rh_w8_merge_rmsnorm /
+// rh_w8_merge_silu) in place of a launch it makes anyway: the split then costs only the
+// reads of its extra ranges, 1.53 us per million partial sums.
+double w8_model_us(int cfg, int T, int K, int N, int ks, bool consumer_merge = false) {
   const int rows = cfg == kTileBig ? 256 : 128, toks = cfg == kWide128 ? 128 : 96;
   const double factor = cfg == kWide128 ? 1.0 : cfg == kWide96 ? 0.8513 : 1.34;
   const double alone = cfg == kWide128 ? 0.8826 : cfg == kWide96 ? 0.9462 : 0.7039;
@@ -469,8 +472,14 @@ double w8_model_us(int cfg, int T, int K, int N, int ks) {
   const double w = (K / 128.0 / ks + 1.8343) * factor;
   const int64_t rounds = (wgs + 255) / 256;
   double t = static_cast<double>(rounds / 2) * 2.0 * w + static_cast<double>(rounds % 2) * w / alone;
+  if (ks > 1 && consumer_merge) return t + 1.5261e-6 * (ks - 1) * static_cast<double>(T) * N;
   if (ks > 1) t += 2.1571 + 1.5261e-6 * (ks + 1) * static_cast<double>(T) * N;
   return t;
+}
+
+int64_t w8_grid(int cfg, int T, int N) {
+  const int rows = cfg == kTileBig ? 256 : 128, toks = cfg == kWide128 ? 128 : 96;
+  return static_cast<int64_t>((N + rows - 1) / rows) * ((T + toks - 1) / toks);
 }
 
 bool w8_wide_fits(int K, int ks) { return K % 128 == 0 && ks <= K / 128; }
@@ -588,6 +597,31 @@ extern "C" int rh_gemm_w8_gate_up_silu(const int8_t* w8, int64_t ldw, const floa
 extern "C" int rh_gemm_w8_plan(int T, int K, int N) {
   if (T < 1 || K <= 0 || K % 64 || N <= 0) return -1;
   return w8_plan(T, K, N).ksplit;
+}
+
+// The split for a product whose consumer merges it. Where the plan runs the product unsplit
+// on fewer than 256 workgroups, the model prices a lone round below what it measures on such
+// grids (Llama-3-8B's o projection, 4096 x 4096 at T = 560: 30 us modelled, 38-44 measured),
+// so there the K is split over the ranges the model prices lowest with the consumer's merge
+// (the o projection takes 3 ranges on the 128 x 128 tile: Llama-3-8B int8 mixed step 21.23 ->
+// 21.10 ms; the down projection's plan, 3 ranges, was already the best of 2-5).
+int w8_partials_plan(int T, int K, int N) {
+  const W8Plan p = w8_plan(T, K, N);
+  if (T <= 64 || K % 128 || N % 4 || p.ksplit > 1 || w8_grid(p.cfg, T, N) >= 256) return p.ksplit;
+  int best = 1;
+  double tb = 0.0;
+  for (int ks = 2; ks <= kMaxW8Split && (K / 128) / ks >= 2; ++ks) {
+    for (int cfg : {kWide128, kWide96}) {
+      const double t = w8_model_us(cfg, T, K, N, ks, true);
+      if (best == 1 || t < tb) tb = t, best = ks;
+    }
+  }
+  return best;
+}
+
+extern "C" int rh_gemm_w8_partials_plan(int T, int K, int N) {
+  if (T < 1 || K <= 0 || K % 64 || N <= 0) return -1;
+  return w8_partials_plan(T, K, N);
 }
 
 extern "C" int rh_gemm_w8_kernel(int T, int K, int N, int ksplit) {

@@ -437,7 +437,7 @@ int HipBackend::w8_partials(const DeviceMatrix& W, const std::uint16_t* x, int T
   if (T <= 64) {
     if (W.N >= 8192 || W.K >= 5000) ks = rh_gemm_w8_split_plan(T, W.K, W.N);
   } else {
-    ks = rh_gemm_w8_plan(T, W.K, W.N);
+    ks = rh_gemm_w8_partials_plan(T, W.K, W.N);
   }
   if (ks < 2) return 0;
   RH_CHECK(rh_gemm_w8_partials(W.i8.p, W.ldw, x, T, W.K, W.N, ks, w8_split_ws(ks, T, W.N), stream_));

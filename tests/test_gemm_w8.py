@@ -124,9 +124,14 @@ def test_plan(dev):
     shapes = ((6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336))
     assert [L.rh_gemm_w8_plan(560, k, n) for n, k in shapes] == [1, 1, 1, 3]
     assert [L.rh_gemm_w8_kernel(560, k, n, L.rh_gemm_w8_plan(560, k, n)) for n, k in shapes] == [2, 3, 1, 2]
+    # merged by the consumer (o, down, gate_up): unsplit grids under 256 workgroups take K ranges
+    assert [L.rh_gemm_w8_partials_plan(560, k, n) for n, k in shapes] == [2, 3, 1, 3]
+    assert L.rh_gemm_w8_kernel(560, 4096, 4096, 3) == 2 and L.rh_gemm_w8_partials_plan(0, 64, 64) == -1
+    assert L.rh_gemm_w8_partials_plan(48, 4096, 4096) == L.rh_gemm_w8_plan(48, 4096, 4096)
     # TinyLlama at 512-token prefill chunks: qkv, wo, gate_up, down
     shapes = ((2560, 2048), (2048, 2048), (11264, 2048), (2048, 5632))
     assert [L.rh_gemm_w8_plan(512, k, n) for n, k in shapes] == [1, 2, 1, 4]
+    assert [L.rh_gemm_w8_partials_plan(512, k, n) for n, k in shapes] == [2, 2, 1, 4]
     assert L.rh_gemm_w8_plan(560, 100, 64) == -1 and L.rh_gemm_w8_plan(0, 64, 64) == -1
     assert L.rh_gemm_w8_plan(100, 128, 4096) == 1  # ranges of at least two 128-k steps
     # K not a multiple of 128: the 64-k step kernels; at most 64 tokens: the 128 x 128 tile
@@ -257,7 +262,7 @@ def test_skinny_accumulates_and_limits(torch_mod, dev):
 
 
 @pytest.mark.parametrize("T,I,H,ks", [(17, 1024, 512, 2), (32, 5632, 2048, 3), (48, 2048, 4096, 8), (100, 1536, 576, 4),
-                                      (200, 1024, 1024, 3)])
+                                      (200, 1024, 1024, 3), (560, 4096, 4096, 3)])
 def test_merge_fused_consumers_equal_the_chain(torch_mod, dev, T, I, H, ks):
     """rh_gemm_w8_partials + rh_w8_merge_silu equals the split product + rh_silu_mul, and
     rh_gemm_w8_partials + rh_w8_merge_rmsnorm equals the split product accumulated into the
