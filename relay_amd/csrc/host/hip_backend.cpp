@@ -435,7 +435,11 @@ int HipBackend::w8_partials(const DeviceMatrix& W, const std::uint16_t* x, int T
   if (!W.i8.p || T <= 16 || W.K % 64 || W.N % 4) return 0;
   int ks = 0;
   if (T <= 64) {
-    if (W.N >= 8192 || W.K >= 5000) ks = rh_gemm_w8_split_plan(T, W.K, W.N);
+    // Narrow matrices (the o projection) too from 25 tokens, where the merge folds the
+    // MLP RMSNorm launch in (TinyLlama int8 decode at 28 / 32 / 40 / 48 / 64 sequences
+    // -0.4..-0.7 / -1.0 / -3.1 / -3.5 / -5.5%, Llama-3-8B int8 48 x 8192 12.49 -> 12.31 ms;
+    // at 17-24 level or slower).
+    if (W.N >= 8192 || W.K >= 5000 || T > 24) ks = rh_gemm_w8_split_plan(T, W.K, W.N);
   } else {
     ks = rh_gemm_w8_partials_plan(T, W.K, W.N);
   }

@@ -234,14 +234,16 @@ def test_library_gemm_choices_agree(dev, monkeypatch):
         assert rel_err_rowmax(got[mode], cpu) < 2e-3, mode
 
 
-def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev):
+@pytest.mark.parametrize("heads,hidden,n_seq", [(4, 256, 20), (8, 512, 32)])
+def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev, heads, hidden, n_seq):
     """Weights of the form q * 2^-9 with a +-127 in every row quantize exactly (scale 2^-9,
     the same q back), so the int8 backend multiplies the same values as the fp16 one and the
     logits may differ only by fp32 summation order (amplified where an activation is rounded
     to fp16 between layers: measured 2e-4; a wrong product would be off by O(1)). intermediate 8192 and 20 decode
     sequences put gate_up (N 16384) and down (K 8192) on the split-K int8 GEMM at 20
-    tokens; the prompts (100 tokens) take the large-tile int8 GEMM with its K split."""
-    w = small_model(64, 4, 2, layers=1, hidden=256, inter=8192, vocab=512, seed=3)
+    tokens; the prompts (100 tokens) take the large-tile int8 GEMM with its K split. At 32
+    sequences the 512 x 512 o projection is split over K as well, merged by the MLP RMSNorm."""
+    w = small_model(64, heads, 2, layers=1, hidden=hidden, inter=8192, vocab=512, seed=3)
     rng = np.random.default_rng(11)
     for L in w.layers:
         for f in ("wqkv", "wo", "w_gate_up", "w_down"):
@@ -249,7 +251,7 @@ def test_int8_paths_match_fp16_on_exactly_quantizable_weights(dev):
             q = rng.integers(-127, 128, size=a.shape).astype(np.float32)
             q[:, 0] = np.where(rng.random(a.shape[0]) < 0.5, 127.0, -127.0)
             np.copyto(a, q * 2.0 ** -9)
-    lens = [5] * 20
+    lens = [5] * n_seq
     nb = blocks_needed(lens, 4)
     a = HipBackend(w, nb, 16, max_batch_tokens=2048, options=FAST)
     b = HipBackend(w, nb, 16, max_batch_tokens=2048, options=HipOptions(False, True))
